@@ -1,0 +1,72 @@
+"""ctypes binding of libkoptim.so, the C-ABI boundary of the HIP kernels.
+
+Every entry point returns an int status: 0 on success, a positive hipError_t
+from the launch, or a negative code for an argument error caught on the host
+before anything was launched. ``call`` raises RuntimeError on any nonzero
+status. There is no fallback: if the library is missing, using an op raises.
+"""
+
+import ctypes
+import os
+
+from .build import LIB_PATH
+
+_c_void_p = ctypes.c_void_p
+_int = ctypes.c_int
+_ll = ctypes.c_longlong
+_f = ctypes.c_float
+
+# name -> argument types (all return c_int). Mirrors include/koptim.h.
+SIGNATURES = {
+    "ko_decode_attn_partial": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll,
+                               _int, _int, _int, _int, _int, _int, _int, _f, _c_void_p,
+                               _c_void_p, _c_void_p],
+    "ko_decode_attn_combine": [_c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _int, _int,
+                               _int, _int, _int, _c_void_p, _c_void_p],
+    "ko_decode_attn": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll, _int,
+                       _int, _int, _int, _int, _int, _int, _f, _c_void_p, _c_void_p, _c_void_p,
+                       _c_void_p],
+}
+
+_ERRORS = {-22: "invalid argument", -34: "size out of range", -95: "unsupported shape"}
+
+_lib = None
+
+
+def lib():
+    """Load the in-tree library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP extension first "
+                "(python -m kernel_optim_amd.build)")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.argtypes = argtypes
+            fn.restype = _int
+        _lib = h
+    return _lib
+
+
+def status_message(code):
+    if code < 0:
+        return _ERRORS.get(code, f"argument error {code}")
+    return f"HIP error {code}"
+
+
+def call(name, *args):
+    st = getattr(lib(), name)(*args)
+    if st != 0:
+        raise RuntimeError(f"{name} failed: {status_message(st)} (status {st})")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device=None):
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream

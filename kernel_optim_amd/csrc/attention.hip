@@ -1,0 +1,413 @@
+// Split-K GQA decode attention for gfx950 (MI355X), with the log-sum-exp
+// combine as a second pass.
+//
+// Replaces engine/kernels/fused.py:138-234 (_decode_attn_kernel,
+// _decode_combine_kernel, DecodeAttention.__call__). Semantics follow that
+// code: T query tokens per sequence at positions kv_len-T .. kv_len-1, causal
+// among themselves (query t sees keys < kv_len-T+t+1), softmax scale 1/sqrt(D),
+// query head h reads KV head h/4, P rounded to bf16 before the PV product,
+// fp32 partials (m, l, acc) merged by a log-sum-exp pass and rounded to bf16.
+//
+// Work decomposition (length-aware, graph-safe): a "unit" is (b, kv_head,
+// c) covering keys [c*U, min((c+1)*U, kv_len_b)). Units are enumerated on the
+// device from kv_len (read from device memory every launch), so sequences of
+// different lengths get proportionally many units and the padded tail of the
+// cache is never read. A fixed grid of wavefronts strides over the unit list.
+//
+// One wavefront per unit. Per 16-key step:
+//   QK^T : 4 x v_mfma_f32_16x16x32_bf16. A = Q (16 rows = the 4 group heads
+//          replicated 4x for T=1), B = K (16 key columns). Every lane ends with
+//          the scores of one key for the 4 heads of its token.
+//   softmax: online, with a wave-uniform running max per (token, head) that is
+//          raised only when a score exceeds it by more than 2^8 (lazy
+//          rescaling); exp2 with the log2(e) folded into the scale.
+//   P    : rounded to bf16 and exchanged through 128*T bytes of LDS.
+//   PV   : v_dot2c_f32_bf16 over key pairs; each lane owns 8 head-dim columns
+//          of 4 keys per step, so V is read with fully coalesced 1 KiB loads.
+#include "ko_common.h"
+
+using namespace ko;
+
+namespace {
+
+constexpr int D = 128;          // head dim
+constexpr int G = 4;            // query heads per KV head
+constexpr int WAVES = 4;        // wavefronts per workgroup
+constexpr float TAU = 8.0f;     // lazy-rescale threshold, log2 units
+constexpr float NEG_BIG = -1.0e30f;
+
+__device__ __forceinline__ int nunits(int len, int unit) {
+  return len > 0 ? (len + unit - 1) / unit : 0;
+}
+__device__ __forceinline__ int seq_len(const int* lens, int b, int off, int cap) {
+  int l = lens[b] + off;
+  return l < cap ? l : cap;
+}
+
+// Number of (b, c) pairs over the whole batch.
+__device__ int count_pairs(const int* lens, int off, int cap, int B, int unit) {
+  const int lane = lane_id();
+  int tot = 0;
+  for (int b0 = 0; b0 < B; b0 += 64) {
+    const int b = b0 + lane;
+    const int n = b < B ? nunits(seq_len(lens, b, off, cap), unit) : 0;
+    tot += readlane(wave_incl_scan(n), 63);
+  }
+  return tot;
+}
+
+// Flattened pair index p -> (b, c).
+__device__ void locate_pair(int p, const int* lens, int off, int cap, int B, int unit,
+                            int& b_out, int& c_out) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int b0 = 0; b0 < B; b0 += 64) {
+    const int b = b0 + lane;
+    const int n = b < B ? nunits(seq_len(lens, b, off, cap), unit) : 0;
+    const int incl = wave_incl_scan(n) + carry;
+    const int tot = readlane(incl, 63);
+    if (p < tot) {
+      const unsigned long long below = __ballot(incl <= p);
+      const int k = uniform(__popcll(below));
+      b_out = b0 + k;
+      c_out = p - readlane(incl - n, k);
+      return;
+    }
+    carry = tot;
+  }
+  b_out = -1;
+  c_out = 0;
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void attn_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int* __restrict__ lens, int len_off, int cap,
+    long long cb, long long ch, int B, int nkv, int unit, int max_units, float scale_log2,
+    float* __restrict__ o_part, float* __restrict__ ml) {
+  __shared__ __align__(16) uint16_t lds_p[WAVES][T][G][16];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;   // key slot of the QK lanes / column chunk of the PV lanes
+  const int g = lane >> 4;   // MFMA k-group / PV key row
+  const int nq = nkv * G;
+  const int W = gridDim.x * WAVES;
+  const int total = count_pairs(lens, len_off, cap, B, unit) * nkv;
+  uint16_t* myp = &lds_p[wave][0][0][0];
+
+  for (int u = blockIdx.x * WAVES + wave; u < total; u += W) {
+    const int pidx = u / nkv;
+    const int kvh = u - pidx * nkv;
+    int b, c;
+    locate_pair(pidx, lens, len_off, cap, B, unit, b, c);
+    b = uniform(b);
+    c = uniform(c);
+    if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
+    const int kv_len = uniform(seq_len(lens, b, len_off, cap));
+    const int k0 = c * unit;
+    const int k1 = min(k0 + unit, kv_len);
+    const uint16_t* kb = kc + (long long)b * cb + (long long)kvh * ch;
+    const uint16_t* vb = vc + (long long)b * cb + (long long)kvh * ch;
+
+    // Q as the MFMA A operand: row r -> (token (r/4)%T, head r%4); lane group
+    // g supplies head-dim elements 32i+8g .. 32i+8g+7 for MFMA i.
+    bf16x8 qa[4];
+    {
+      const int trow = (r >> 2) % T;
+      const uint16_t* qrow =
+          q + ((long long)(b * T + trow) * nq + kvh * G + (r & 3)) * D + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, ldg16(qrow + 32 * i));
+    }
+    const int tq = g % T;                           // token of this lane's score rows
+    const int lim = min(k1, kv_len - T + tq + 1);   // exclusive causal key limit
+
+    float mu[T][G];
+    float acc[T][G][8];
+    float lsum[G];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        mu[t][j] = NEG_BIG;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[t][j][e] = 0.f;
+      }
+#pragma unroll
+    for (int j = 0; j < G; ++j) lsum[j] = 0.f;
+
+    auto load_k = [&](int kk, uint4* kr) {
+      const int key = min(kk + r, k1 - 1);
+      const uint16_t* p = kb + (long long)key * D + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[i] = ldg16_stream(p + 32 * i);
+    };
+    auto load_v = [&](int kk, uint4* vr) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key = min(kk + g + 4 * s, k1 - 1);
+        vr[s] = ldg16_stream(vb + (long long)key * D + 8 * r);
+      }
+    };
+
+    auto step = [&](int kk, const uint4* kr, const uint4* vr) {
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8, kr[i]),
+                                                     sc, 0, 0, 0);
+      const bool valid = (kk + r) < lim;
+      float s[G], mrow[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        s[j] = valid ? sc[j] * scale_log2 : -INFINITY;
+        float m = mu[0][j];
+#pragma unroll
+        for (int t = 1; t < T; ++t) m = (tq == t) ? mu[t][j] : m;
+        mrow[j] = m;
+      }
+      bool need = false;
+#pragma unroll
+      for (int j = 0; j < G; ++j) need |= s[j] > mrow[j] + TAU;
+      if (__ballot(need)) {
+        float rm[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) rm[j] = row_max16(s[j]);
+        float alpha[T][G];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            const float mn = fmaxf(mu[t][j], readlane(rm[j], 16 * t));
+            alpha[t][j] = __builtin_amdgcn_exp2f(mu[t][j] - mn);
+            mu[t][j] = mn;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[t][j][e] *= alpha[t][j];
+          }
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          float a = alpha[0][j], m = mu[0][j];
+#pragma unroll
+          for (int t = 1; t < T; ++t) {
+            a = (tq == t) ? alpha[t][j] : a;
+            m = (tq == t) ? mu[t][j] : m;
+          }
+          lsum[j] *= a;
+          mrow[j] = m;
+        }
+      }
+      float pf[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        pf[j] = __builtin_amdgcn_exp2f(s[j] - mrow[j]);
+        lsum[j] += pf[j];
+      }
+      // P (bf16) -> LDS, key order permuted so that a PV lane's 4 keys
+      // (g, g+4, g+8, g+12) are contiguous.
+      const int pos = (r & 3) * 4 + (r >> 2);
+      if (T == 1) {
+        const float v = g == 0 ? pf[0] : g == 1 ? pf[1] : g == 2 ? pf[2] : pf[3];
+        myp[g * 16 + pos] = f32_to_bf16(v);
+      } else if (g < T) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) myp[(g * G + j) * 16 + pos] = f32_to_bf16(pf[j]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint2 pw[T][G];
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+          pw[t][j] = *reinterpret_cast<const uint2*>(myp + (t * G + j) * 16 + 4 * g);
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        const uint32_t xs[4] = {vr[2 * sp].x, vr[2 * sp].y, vr[2 * sp].z, vr[2 * sp].w};
+        const uint32_t ys[4] = {vr[2 * sp + 1].x, vr[2 * sp + 1].y, vr[2 * sp + 1].z,
+                                vr[2 * sp + 1].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = (xs[e] & 0xffffu) | (ys[e] << 16);
+          const uint32_t hi = (xs[e] >> 16) | (ys[e] & 0xffff0000u);
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+              const uint32_t pword = sp ? pw[t][j].y : pw[t][j].x;
+              acc[t][j][2 * e] = dot2_bf16(pword, lo, acc[t][j][2 * e]);
+              acc[t][j][2 * e + 1] = dot2_bf16(pword, hi, acc[t][j][2 * e + 1]);
+            }
+        }
+      }
+      // The next step overwrites this wave's P slot; LDS ops of one wave
+      // execute in order, so the reads above complete first.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    };
+
+    // Two-deep software pipeline over 16-key steps.
+    uint4 ka[4], va[4], kb2[4], vb2[4];
+    load_k(k0, ka);
+    load_v(k0, va);
+    for (int kk = k0; kk < k1; kk += 32) {
+      load_k(kk + 16, kb2);
+      load_v(kk + 16, vb2);
+      step(kk, ka, va);
+      if (kk + 16 >= k1) break;
+      load_k(kk + 32, ka);
+      load_v(kk + 32, va);
+      step(kk + 16, kb2, vb2);
+    }
+
+    // ---- unit epilogue: reduce and write the fp32 partials ----
+    float lrow[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) lrow[j] = row_sum16(lsum[j]);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float v = acc[t][j][e];
+          v += __shfl_xor(v, 16, 64);
+          v += __shfl_xor(v, 32, 64);
+          acc[t][j][e] = v;
+        }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const long long R = (long long)(b * T + t) * nq + kvh * G + g;
+      float* dst = o_part + (R * max_units + c) * D + 8 * r;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (g == j) {
+          reinterpret_cast<float4*>(dst)[0] =
+              make_float4(acc[t][j][0], acc[t][j][1], acc[t][j][2], acc[t][j][3]);
+          reinterpret_cast<float4*>(dst)[1] =
+              make_float4(acc[t][j][4], acc[t][j][5], acc[t][j][6], acc[t][j][7]);
+        }
+      }
+    }
+    if (g < T && r < G) {
+      float m = mu[0][0], l = lrow[0];
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          m = (g == t && r == j) ? mu[t][j] : m;
+          l = (r == j) ? lrow[j] : l;
+        }
+      const long long R = (long long)(b * T + g) * nq + kvh * G + r;
+      reinterpret_cast<float2*>(ml)[R * max_units + c] = make_float2(m, l);
+    }
+  }
+}
+
+// One wavefront per output row (b, t, q_head): log-sum-exp merge of the
+// unit partials, normalise, round to bf16.
+__global__ __launch_bounds__(256) void attn_combine_kernel(
+    const float* __restrict__ o_part, const float* __restrict__ ml,
+    const int* __restrict__ lens, int len_off, int cap, int T, int nq, int rows, int unit,
+    int max_units, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int R = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (R >= rows) return;
+  const int b = R / (T * nq);
+  const int n = nunits(seq_len(lens, b, len_off, cap), unit);
+  const float2* mlr = reinterpret_cast<const float2*>(ml) + (long long)R * max_units;
+  float M = NEG_BIG;
+  for (int c = lane; c < n; c += 64) M = fmaxf(M, mlr[c].x);
+  M = wave_max(M);
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  const float* op = o_part + (long long)R * max_units * D + 2 * lane;
+  for (int c = 0; c < n; ++c) {
+    const float2 mlc = mlr[c];
+    const float w = __builtin_amdgcn_exp2f(mlc.x - M);
+    L += w * mlc.y;
+    const float2 a = *reinterpret_cast<const float2*>(op + (long long)c * D);
+    o0 += w * a.x;
+    o1 += w * a.y;
+  }
+  const float r0 = L > 0.f ? o0 / L : 0.f;
+  const float r1 = L > 0.f ? o1 / L : 0.f;
+  reinterpret_cast<uint32_t*>(out + (long long)R * D)[lane] = pack_bf16x2(r0, r1);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_attn_args(const void* q, const void* kc, const void* vc, const int* lens, int cap,
+                    long long cb, long long ch, int B, int T, int nkv, int head_dim, int unit,
+                    int max_units, const float* o_part, const float* ml) {
+  if (!q || !kc || !vc || !lens || !o_part || !ml) return KO_EINVAL;
+  if (head_dim != D) return KO_ENOTSUP;
+  if (T < 1 || T > 4) return KO_ENOTSUP;
+  if (B < 1 || nkv < 1 || cap < 1) return KO_EINVAL;
+  if (unit < 16 || (unit & 15)) return KO_EINVAL;
+  if ((long long)max_units * unit < cap) return KO_ERANGE;
+  if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(o_part)) return KO_EINVAL;
+  if ((cb & 7) || (ch & 7) || cb < 0 || ch < 0) return KO_EINVAL;
+  return KO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ko_decode_attn_partial(const void* q, const void* k_cache, const void* v_cache,
+                           const int* kv_lens, int len_offset, int cap,
+                           long long cache_b_stride, long long cache_h_stride, int B, int T,
+                           int nkv, int head_dim, int unit, int max_units, int grid_waves,
+                           float scale, float* o_part, float* ml, void* stream) {
+  int st = check_attn_args(q, k_cache, v_cache, kv_lens, cap, cache_b_stride, cache_h_stride,
+                           B, T, nkv, head_dim, unit, max_units, o_part, ml);
+  if (st) return st;
+  if (grid_waves < 1) return KO_EINVAL;
+  const dim3 grid((grid_waves + WAVES - 1) / WAVES), block(64 * WAVES);
+  const float sl2 = scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* qq = static_cast<const uint16_t*>(q);
+  const uint16_t* kk = static_cast<const uint16_t*>(k_cache);
+  const uint16_t* vv = static_cast<const uint16_t*>(v_cache);
+#define KO_ATTN_LAUNCH(TT)                                                                   \
+  hipLaunchKernelGGL(attn_partial_kernel<TT>, grid, block, 0, s, qq, kk, vv, kv_lens,        \
+                     len_offset, cap, cache_b_stride, cache_h_stride, B, nkv, unit, max_units, \
+                     sl2, o_part, ml)
+  switch (T) {
+    case 1: KO_ATTN_LAUNCH(1); break;
+    case 2: KO_ATTN_LAUNCH(2); break;
+    case 3: KO_ATTN_LAUNCH(3); break;
+    default: KO_ATTN_LAUNCH(4); break;
+  }
+#undef KO_ATTN_LAUNCH
+  return KO_LAUNCH_STATUS();
+}
+
+int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_lens,
+                           int len_offset, int cap, int B, int T, int nq, int head_dim, int unit,
+                           int max_units, void* out, void* stream) {
+  if (!o_part || !ml || !kv_lens || !out) return KO_EINVAL;
+  if (head_dim != D) return KO_ENOTSUP;
+  if (B < 1 || T < 1 || nq < 1 || unit < 1 || (long long)max_units * unit < cap) return KO_EINVAL;
+  if (!aligned16(out)) return KO_EINVAL;
+  const int rows = B * T * nq;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((rows + WAVES - 1) / WAVES), dim3(64 * WAVES), 0,
+                     static_cast<hipStream_t>(stream), o_part, ml, kv_lens, len_offset, cap, T,
+                     nq, rows, unit, max_units, static_cast<uint16_t*>(out));
+  return KO_LAUNCH_STATUS();
+}
+
+int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens,
+                   int len_offset, int cap, long long cache_b_stride, long long cache_h_stride,
+                   int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,
+                   float scale, float* o_part, float* ml, void* out, void* stream) {
+  int st = ko_decode_attn_partial(q, k_cache, v_cache, kv_lens, len_offset, cap, cache_b_stride,
+                                  cache_h_stride, B, T, nkv, head_dim, unit, max_units,
+                                  grid_waves, scale, o_part, ml, stream);
+  if (st) return st;
+  return ko_decode_attn_combine(o_part, ml, kv_lens, len_offset, cap, B, T, nkv * G, head_dim,
+                                unit, max_units, out, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+"""The C-ABI library: it builds, loads without a GPU, exports every entry point
+include/koptim.h declares, and rejects bad arguments on the host (no compute
+calls here)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "koptim.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\bint\s+(ko_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def libpath():
+    import kernel_optim_amd.build as B
+    if not os.path.exists(B.LIB_PATH):
+        B.build()
+    return B.LIB_PATH
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "ko_decode_attn" in names and len(names) >= 3
+
+
+def test_library_exports_every_declared_symbol(libpath):
+    out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\sT\s+(ko_\w+)", out))
+    missing = [n for n in declared() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_ctypes_binding_covers_header(libpath):
+    from kernel_optim_amd import _lib
+    assert sorted(_lib.SIGNATURES) == declared()
+    h = _lib.lib()
+    for name in declared():
+        assert isinstance(getattr(h, name), ctypes._CFuncPtr)
+
+
+def test_host_side_argument_errors_without_gpu(libpath):
+    """Null pointers / unsupported shapes are refused before any launch, so these
+    calls are safe on a machine without a GPU."""
+    from kernel_optim_amd import _lib
+    h = _lib.lib()
+    st = h.ko_decode_attn_partial(None, None, None, None, 1, 64, 0, 0, 1, 1, 8, 128, 64, 1, 1,
+                                  0.1, None, None, None)
+    assert st == -22
+    fake = 1 << 20  # never dereferenced: the shape check fails first
+    st = h.ko_decode_attn_partial(fake, fake, fake, fake, 1, 64, 0, 0, 1, 1, 8, 64, 64, 1, 1,
+                                  0.1, fake, fake, None)
+    assert st == -95
+    st = h.ko_decode_attn_partial(fake, fake, fake, fake, 1, 64, 0, 0, 1, 1, 8, 128, 64, 0, 1,
+                                  0.1, fake, fake, None)
+    assert st == -34
+
+
+def test_wrapper_raises_runtime_error_on_status():
+    from kernel_optim_amd import _lib
+    assert "invalid argument" in _lib.status_message(-22)
+    with pytest.raises(RuntimeError):
+        _lib.call("ko_decode_attn_partial", None, None, None, None, 1, 64, 0, 0, 1, 1, 8, 128,
+                  64, 1, 1, 0.1, None, None, None)

@@ -1,0 +1,187 @@
+"""GPU parity of the HIP split-K GQA decode attention against the CPU oracle
+(engine/kernels/fused.py:138-234 semantics). Tolerance: atol = rtol = 2e-2
+against fp32/fp64 references, bf16 inputs."""
+
+import pytest
+import torch
+
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=2e-2, atol=2e-2)
+
+
+def _fused():
+    from kernel_optim_amd.kernels import fused
+    return fused
+
+
+def _inputs(B, T, cap, dev, seeds=(0, 1, 2), nq=32, nkv=8, D=128):
+    gq, gk, gv = (torch.Generator(device=dev).manual_seed(s) for s in seeds)
+    q = torch.randn(B * T, nq * D, device=dev, generator=gq).to(torch.bfloat16)
+    k = torch.randn(B, nkv, cap, D, device=dev, generator=gk).to(torch.bfloat16)
+    v = torch.randn(B, nkv, cap, D, device=dev, generator=gv).to(torch.bfloat16)
+    return q, k, v
+
+
+def _gpu_ref_fp32(q, k, v, lens, T=1):
+    """Plain PyTorch fp32 attention on the GPU (per sequence, GQA by grouping)."""
+    B, nkv, cap, D = k.shape
+    nq = q.shape[1] // D
+    out = torch.empty(B * T, nq * D, device=q.device, dtype=torch.float32)
+    qv = q.float().view(B, T, nkv, nq // nkv, D)
+    for b in range(B):
+        L = int(lens[b])
+        kk = k[b, :, :L].float()                               # [nkv, L, D]
+        vv = v[b, :, :L].float()
+        qq = qv[b].permute(1, 0, 2, 3).reshape(nkv, -1, D).contiguous()   # [nkv, T*4, D]
+        s = torch.bmm(qq, kk.transpose(1, 2).contiguous()) * D ** -0.5    # [nkv, T*4, L]
+        s = s.view(nkv, T, nq // nkv, L)
+        keys = torch.arange(L, device=q.device)
+        for t in range(T):
+            s[:, t, :, keys > L - T + t] = float("-inf")
+        p = torch.softmax(s.view(nkv, -1, L), dim=-1)
+        o = torch.bmm(p, vv).view(nkv, T, nq // nkv, D).permute(1, 0, 2, 3)
+        out.view(B, T, nq, D)[b] = o.reshape(T, nq, D)
+    return out
+
+
+def test_config1_b1_ctx512(dev):
+    """Config 1 shape: B=1, 32q/8kv, d=128, ctx 512, seeds q=0 k=1 v=2."""
+    fused = _fused()
+    q, k, v = _inputs(1, 1, 512, dev)
+    pos = torch.tensor([511], dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(1, 1, 512, 32, 8, 128, dev)
+    att(q, k, v, pos, out)
+    torch.cuda.synchronize()
+    want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [512])
+    torch.testing.assert_close(out.cpu().double(), want, **TOL)
+
+
+@pytest.mark.parametrize("unit", [16, 64, 512])
+def test_ragged_small_against_oracle(dev, unit):
+    fused = _fused()
+    B, cap = 6, 320
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(4, 5, 6))
+    lens = [1, 15, 16, 17, 300, 320]
+    pos = torch.tensor([x - 1 for x in lens], dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev, unit=unit)
+    att(q, k, v, pos, out)
+    torch.cuda.synchronize()
+    want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), lens)
+    torch.testing.assert_close(out.cpu().double(), want, **TOL)
+
+
+@pytest.mark.parametrize("T", [2, 3, 4])
+def test_multi_token_causal(dev, T):
+    fused = _fused()
+    B, cap = 3, 200
+    q, k, v = _inputs(B, T, cap, dev, seeds=(7, 8, 9))
+    first = [0, 37, 200 - T]
+    pos = torch.tensor(first, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, T, cap, 32, 8, 128, dev, unit=32)
+    att(q, k, v, pos, out)
+    torch.cuda.synchronize()
+    want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [p + T for p in first], T=T)
+    torch.testing.assert_close(out.cpu().double(), want, **TOL)
+
+
+def test_config2_b16_ctx8192(dev):
+    """Config 2: B=16 x 8192, against fp32 torch on the GPU for every sequence and
+    the fp64 CPU oracle for four of them."""
+    fused = _fused()
+    B, cap = 16, 8192
+    q, k, v = _inputs(B, 1, cap, dev)
+    pos = torch.full((B,), cap - 1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev)
+    att(q, k, v, pos, out)
+    torch.cuda.synchronize()
+    ref = _gpu_ref_fp32(q, k, v, [cap] * B)
+    torch.testing.assert_close(out.float(), ref, **TOL)
+    sel = [0, 5, 10, 15]
+    want = A.decode_attention(q.view(B, -1)[sel].cpu(), k[sel].cpu(), v[sel].cpu(), [cap] * 4)
+    torch.testing.assert_close(out.view(B, -1)[sel].cpu().double(), want, **TOL)
+
+
+def test_config3_ragged_padded_tail_unread(dev):
+    """Config 3: B=64, lengths ~ U[128, 16384] (seed 3), cache padded to 16384. The
+    padded tail is filled with NaN: reading any of it would poison the output."""
+    fused = _fused()
+    B, cap = 64, 16384
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(128, cap + 1, (B,), generator=g, dtype=torch.int32)
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(10, 11, 12))
+    for b in range(B):
+        k[b, :, int(lens[b]):] = float("nan")
+        v[b, :, int(lens[b]):] = float("nan")
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev)
+    att.with_lengths(q, k, v, lens.to(dev), out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    ref = _gpu_ref_fp32(q, k, v, lens.tolist())
+    torch.testing.assert_close(out.float(), ref, **TOL)
+
+
+def test_deterministic_and_unit_invariant(dev):
+    fused = _fused()
+    B, cap = 4, 3000
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(13, 14, 15))
+    pos = torch.tensor([2999, 100, 2048, 1500], dtype=torch.int32, device=dev)
+    outs = []
+    for unit in (64, 256, 1024):
+        att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev, unit=unit)
+        o1, o2 = torch.empty_like(q), torch.empty_like(q)
+        att(q, k, v, pos, o1)
+        att(q, k, v, pos, o2)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2)
+        outs.append(o1.float())
+    for o in outs[1:]:
+        torch.testing.assert_close(o, outs[0], **TOL)
+
+
+def test_graph_replay_tracks_device_positions(dev):
+    fused = _fused()
+    B, cap = 2, 1024
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(16, 17, 18))
+    pos = torch.tensor([10, 500], dtype=torch.int32, device=dev)
+    out = torch.zeros_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        att(q, k, v, pos, out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        att(q, k, v, pos, out)
+    for p in ([10, 500], [700, 3], [1023, 1023]):
+        pos.copy_(torch.tensor(p, dtype=torch.int32))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = torch.empty_like(q)
+        att(q, k, v, pos, eager)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [x + 1 for x in p])
+        torch.testing.assert_close(out.cpu().double(), want, **TOL)
+
+
+def test_bad_arguments_raise_before_launch(dev):
+    fused = _fused()
+    q, k, v = _inputs(1, 1, 64, dev)
+    att = fused.DecodeAttention(1, 1, 64, 32, 8, 128, dev)
+    pos = torch.tensor([3], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        att(q, k, v, pos.long(), torch.empty_like(q))
+    with pytest.raises(ValueError):
+        att(q.float(), k, v, pos, torch.empty_like(q))
+    with pytest.raises(ValueError):
+        att(q, k[:, :, :32], v, pos, torch.empty_like(q))
