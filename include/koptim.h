@@ -51,6 +51,72 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
                    int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,
                    float scale, float* o_part, float* ml, void* out, void* stream);
 
+/* ---- residual add + RMSNorm ---------------------------------------------
+ * Replaces engine/kernels/fused.py:16-36 (_add_rms_norm_kernel) as launched by
+ * add_rms_norm (fused.py:39-46). res [rows, n] bf16 (updated in place to
+ * bf16(res + delta) when delta != NULL), weight [n], out [rows, n];
+ * out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))). n % 8 == 0, n <= 8192. */
+int ko_add_rms_norm(void* res, const void* delta, const void* weight, void* out, int rows, int n,
+                    float eps, void* stream);
+
+/* ---- per-head q/k RMSNorm + RoPE + KV-cache append ----------------------
+ * Replaces engine/kernels/fused.py:54-96 (_qk_norm_rope_kernel) as launched by
+ * qk_norm_rope (fused.py:99-106). qkv [M, (nq+2nkv)*d] bf16, M = B*T; row m is
+ * sequence m/T at position pos[m/T] + m%T. Writes q_out [M, nq*d], and k
+ * (normed + roped) / v (raw) into one cache layer [B, nkv, cap, d] at that
+ * position. cos/sin [rows, d] bf16 tables. Positions outside [0, max_pos)
+ * (max_pos = min(cap, table rows)) are skipped. d == 128. */
+int ko_qk_norm_rope(const void* qkv, const void* q_w, const void* k_w, const void* cos,
+                    const void* sin, const int* pos, void* q_out, void* k_cache, void* v_cache,
+                    int M, int T, long long cache_b_stride, long long cache_h_stride, float eps,
+                    int nq, int nkv, int d, int max_pos, void* stream);
+
+/* Same from the fp32 QKV accumulator acc [B, (nq+2nkv)*d] (T = 1): rounds it to
+ * bf16 first, re-zeroes it, and zeroes zero_buf[0..n_zero).
+ * Replaces engine/kernels/gemv.py:219-268 (_qk_norm_rope_acc_kernel) as launched
+ * by qk_norm_rope_acc (gemv.py:271-277). */
+int ko_qk_norm_rope_acc(float* acc, const void* q_w, const void* k_w, const void* cos,
+                        const void* sin, const int* pos, void* q_out, void* k_cache,
+                        void* v_cache, float* zero_buf, int n_zero, int B,
+                        long long cache_b_stride, long long cache_h_stride, float eps, int nq,
+                        int nkv, int d, int max_pos, void* stream);
+
+/* ---- SwiGLU ---------------------------------------------------------------
+ * Replaces engine/kernels/fused.py:112-120 (_silu_mul_kernel) as launched by
+ * silu_mul (fused.py:123-127): gu [M, 2I] (gate | up) bf16 ->
+ * out [M, I] = bf16(bf16(silu(gate)) * up). I % 8 == 0. */
+int ko_silu_mul(const void* gu, void* out, int M, int I, void* stream);
+
+/* ---- embedding gather + sum of squares ------------------------------------
+ * Replaces engine/kernels/gemv.py:201-211 (_embed_ss_kernel) as launched by
+ * embed_ss (gemv.py:214-216): h[m] = emb[ids[m]] ([V, H] bf16, ids int64),
+ * ss[m] = sum(h[m]^2) fp32 (ss may be NULL). Ids outside [0, V) gather zeros. */
+int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M, int H, int V,
+                void* stream);
+
+/* ---- fused skinny GEMM ------------------------------------------------------
+ * Replaces engine/kernels/gemv.py:30-106 (_gemv_kernel) as launched by
+ * Gemv.__call__ (gemv.py:140-150): y[M, N] = x[M, K] @ W[N, K]^T, bf16 in,
+ * fp32 accumulate, every weight read once for all M rows.
+ * norm != 0: x <- bf16(nw * bf16(x * rsqrt(ss/K + eps))); ss == NULL computes
+ *            the row sums of squares from x.
+ * epi 0 F32    y fp32 [M, N] (stored; atomically added if accumulate != 0)
+ *     1 BF16   y bf16 [M, N]
+ *     2 RESID  h [M, N] bf16 <- bf16(h + bf16(acc)); ss_out[m] += sum(h^2) if given
+ *     3 SWIGLU w [2N, K] (gate | up); y bf16 = bf16(bf16(silu(bf16 g)) * bf16 u)
+ *     4 ARGMAX ids[m] (int64) = argmax_n bf16(acc) with lowest index on ties
+ *              (torch.argmax at engine/engine.py:291, fused into the LM head);
+ *              bf16 logits stored in y when y != NULL; part/counter are
+ *              scratch (ko_gemv_argmax_scratch floats, one int zeroed once).
+ * rows_per_wg: 4 or 8 output columns per 256-thread workgroup. K % 8 == 0. */
+int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
+            float* ss_out, long long* ids, float* part, int* counter, int M, int N, int K,
+            int epi, int norm, int accumulate, int rows_per_wg, float eps, void* stream);
+
+/* Number of fp32 scratch elements EPI 4 needs for N columns (a size, not a
+ * status; -1 for bad arguments). Helper of ko_gemv, no reference counterpart. */
+long long ko_gemv_argmax_scratch(int N, int rows_per_wg);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,23 @@ SIGNATURES = {
     "ko_decode_attn": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll, _int,
                        _int, _int, _int, _int, _int, _int, _f, _c_void_p, _c_void_p, _c_void_p,
                        _c_void_p],
+    "ko_add_rms_norm": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _f, _c_void_p],
+    "ko_qk_norm_rope": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                        _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll, _f, _int, _int,
+                        _int, _int, _c_void_p],
+    "ko_qk_norm_rope_acc": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll,
+                            _f, _int, _int, _int, _int, _c_void_p],
+    "ko_silu_mul": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
+    "ko_embed_ss": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _c_void_p],
+    "ko_gemv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _int, _int, _int, _int, _f,
+                _c_void_p],
+    "ko_gemv_argmax_scratch": [_int, _int],
 }
+
+# Entry points whose return value is a size, not a status.
+RESTYPES = {"ko_gemv_argmax_scratch": _ll}
 
 _ERRORS = {-22: "invalid argument", -34: "size out of range", -95: "unsupported shape"}
 
@@ -45,7 +61,7 @@ def lib():
         for name, argtypes in SIGNATURES.items():
             fn = getattr(h, name)
             fn.argtypes = argtypes
-            fn.restype = _int
+            fn.restype = RESTYPES.get(name, _int)
         _lib = h
     return _lib
 

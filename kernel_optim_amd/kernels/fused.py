@@ -104,3 +104,55 @@ class DecodeAttention:
         """Ragged form: lengths[b] = number of valid keys of sequence b (int32);
         the T queries sit at positions lengths[b]-T .. lengths[b]-1."""
         self._run(q, k_cache, v_cache, lengths, 0, out)
+
+
+# ---------------------------------------------------------------------------
+# Residual add + RMSNorm (fused.py:16-46).
+# ---------------------------------------------------------------------------
+def add_rms_norm(res, delta, weight, out, eps):
+    """out = rmsnorm(res + delta); res <- res + delta (bf16). Rows contiguous [M, N],
+    N a multiple of 8 and at most 8192."""
+    n_rows, n_cols = res.shape
+    _check(res, "res", BF16)
+    if delta is not None:
+        _check(delta, "delta", BF16, (n_rows, n_cols))
+    _check(weight, "weight", BF16, (n_cols,))
+    _check(out, "out", BF16, (n_rows, n_cols))
+    _lib.call("ko_add_rms_norm", _lib.ptr(res), _lib.ptr(delta), _lib.ptr(weight), _lib.ptr(out),
+              n_rows, n_cols, eps, _lib.stream_ptr())
+
+
+# ---------------------------------------------------------------------------
+# Per-head q/k RMSNorm + RoPE, writing K/V straight into the cache (fused.py:49-106).
+# ---------------------------------------------------------------------------
+def qk_norm_rope(qkv, q_w, k_w, cos, sin, pos, q_out, k_cache, v_cache, T, eps, nq, nkv, d):
+    """qkv: [M, (nq+2nkv)*d] bf16 with M = B*T rows (row m is batch m//T at position
+    pos[b] + m%T); k_cache/v_cache: one layer, [B, nkv, cap, d]."""
+    M = qkv.shape[0]
+    _need(M % T == 0, "rows must be B*T")
+    B = M // T
+    _check(qkv, "qkv", BF16, (M, (nq + 2 * nkv) * d))
+    _check(q_out, "q_out", BF16, (M, nq * d))
+    _check(q_w, "q_w", BF16, (d,))
+    _check(k_w, "k_w", BF16, (d,))
+    _check(cos, "cos", BF16)
+    _check(sin, "sin", BF16)
+    _check(pos, "pos", torch.int32, (B,))
+    _check_cache(k_cache, "k_cache", B, nkv, k_cache.shape[2], d)
+    _check_cache(v_cache, "v_cache", B, nkv, k_cache.shape[2], d)
+    _need(k_cache.stride() == v_cache.stride(), "k_cache and v_cache must share strides")
+    _lib.call("ko_qk_norm_rope", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w), _lib.ptr(cos),
+              _lib.ptr(sin), _lib.ptr(pos), _lib.ptr(q_out), _lib.ptr(k_cache), _lib.ptr(v_cache),
+              M, T, k_cache.stride(0), k_cache.stride(1), eps, nq, nkv, d,
+              min(k_cache.shape[2], cos.shape[0], sin.shape[0]), _lib.stream_ptr())
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU: out = bf16(bf16(silu(gate)) * up), gate/up as [M, 2*I] (fused.py:109-127).
+# ---------------------------------------------------------------------------
+def silu_mul(gu, out):
+    M, two_i = gu.shape
+    I = two_i // 2
+    _check(gu, "gu", BF16, (M, 2 * I))
+    _check(out, "out", BF16, (M, I))
+    _lib.call("ko_silu_mul", _lib.ptr(gu), _lib.ptr(out), M, I, _lib.stream_ptr())

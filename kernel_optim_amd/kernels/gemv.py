@@ -1,0 +1,169 @@
+"""Fused skinny GEMMs for the decode step on hand-written HIP kernels (gfx950).
+
+Python surface of the reference's engine/kernels/gemv.py:
+- ``EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3``        (gemv.py:27)
+- ``Gemv(M, N, K, epi, norm, allow_split=False, eps=1e-6)``          (gemv.py:109-120)
+  ``__call__(x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None)``
+                                                                    (gemv.py:140-150)
+  ``candidates()``, ``tune(weights, deadline)``                      (gemv.py:122-195)
+- ``embed_ss(ids, emb, h, ss)``                                      (gemv.py:214-216)
+- ``qk_norm_rope_acc(acc, q_w, k_w, cos, sin, pos, q_out, k_cache, v_cache,
+  zero_buf, eps, nq, nkv, d)``                                       (gemv.py:271-277)
+
+Additions of this backend:
+- ``EPI_ARGMAX = 4``: the LM head with greedy selection fused in; pass ``ids``
+  ([M] int64) and optionally ``y`` for the bf16 logits.
+- NORM with ``ss=None`` computes the row's sum of squares from x inside the
+  kernel (no separate sum-of-squares buffer or zeroing discipline needed).
+
+``cfg`` is an opaque tuple ``(rows_per_workgroup,)``. ``allow_split`` is
+accepted for signature compatibility; this kernel never splits K (each
+workgroup streams full rows), so the F32 epilogue is a plain store.
+"""
+
+import time
+
+import torch
+
+from .. import _lib
+from .fused import BF16, _check, _need
+
+EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3, 4
+
+
+class Gemv:
+    """One fused projection y[M, N] = x[M, K] @ W[N, K]^T with a norm prologue and
+    an epilogue; its launch config is picked by GPU timing at setup."""
+
+    def __init__(self, M, N, K, epi, norm, allow_split=False, eps=1e-6):
+        _need(epi in (EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX), f"bad epilogue {epi}")
+        _need(K % 8 == 0, "K must be a multiple of 8")
+        self.M, self.N, self.K, self.epi, self.norm, self.eps = M, N, K, epi, bool(norm), eps
+        self.allow_split = allow_split
+        self.cfg = self.candidates()[0]
+        self._part = None
+        self._counter = None
+        self.us = float("nan")
+
+    def candidates(self):
+        """Rows per workgroup: 4 keeps more workgroups in flight for small N,
+        8 halves the per-workgroup norm prologue for large N."""
+        if self.epi == EPI_ARGMAX or self.N >= 32768:
+            return [(8,), (4,)]
+        return [(4,), (8,)]
+
+    def _scratch(self, device):
+        if self._part is None or self._part.device != device:
+            n = _lib.lib().ko_gemv_argmax_scratch(self.N, 4)
+            self._part = torch.empty(max(n, 2), dtype=torch.float32, device=device)
+            self._counter = torch.zeros(1, dtype=torch.int32, device=device)
+        return self._part, self._counter
+
+    def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None):
+        M, N, K, epi = self.M, self.N, self.K, self.epi
+        (rows,) = cfg or self.cfg
+        _check(x, "x", BF16, (M, K))
+        _check(w, "w", BF16, ((2 * N) if epi == EPI_SWIGLU else N, K))
+        if self.norm:
+            _check(nw, "nw", BF16, (K,))
+            if ss is not None:
+                _check(ss, "ss", torch.float32, (M,))
+        if epi == EPI_F32:
+            _check(y, "y", torch.float32, (M, N))
+        elif epi in (EPI_BF16, EPI_SWIGLU):
+            _check(y, "y", BF16, (M, N))
+        elif epi == EPI_RESID:
+            _check(h, "h", BF16, (M, N))
+            if ss_out is not None:
+                _check(ss_out, "ss_out", torch.float32, (M,))
+        else:
+            _check(ids, "ids", torch.int64, (M,))
+            if y is not None:
+                _check(y, "y", BF16, (M, N))
+        part = counter = None
+        if epi == EPI_ARGMAX:
+            part, counter = self._scratch(x.device)
+        _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
+                  _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
+                  _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(part), _lib.ptr(counter),
+                  M, N, K, epi, int(self.norm), 0, rows, self.eps, _lib.stream_ptr())
+
+    def tune(self, weights, deadline):
+        """Pick the fastest candidate by GPU time: one call per layer weight (cold),
+        captured in a graph and replayed twice (gemv.py:152-195)."""
+        dev = weights[0].device
+        M, N, K = self.M, self.N, self.K
+        x = torch.randn(M, K, device=dev, dtype=BF16)
+        y = torch.zeros(M, N, device=dev, dtype=torch.float32 if self.epi == EPI_F32 else BF16)
+        nw = torch.ones(K, device=dev, dtype=BF16)
+        h = torch.zeros(M, N, device=dev, dtype=BF16)
+        ids = torch.zeros(M, device=dev, dtype=torch.int64)
+        kw = dict(y=y, nw=nw, h=h, ids=ids)
+        best = None
+        for cfg in self.candidates():
+            if time.monotonic() > deadline:
+                break
+            try:
+                self(x, weights[0], cfg=cfg, **kw)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for wt in weights:
+                        self(x, wt, cfg=cfg, **kw)
+                g.replay()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                g.replay()
+                g.replay()
+                b.record()
+                torch.cuda.synchronize()
+                t = a.elapsed_time(b)
+                del g
+            except RuntimeError:
+                torch.cuda.synchronize()
+                continue
+            if best is None or t < best[0]:
+                best = (t, cfg)
+        if best is not None:
+            self.cfg = best[1]
+            self.us = best[0] / (2 * len(weights)) * 1e3
+        return self.cfg
+
+
+def embed_ss(ids, emb, h, ss):
+    """h[m] = emb[ids[m]]; ss[m] = sum(h[m]^2) (gemv.py:201-216). ss may be None."""
+    M, H = h.shape
+    _check(ids, "ids", torch.int64, (M,))
+    _check(emb, "emb", BF16)
+    _need(emb.dim() == 2 and emb.shape[1] == H, "emb must be [V, H]")
+    _check(h, "h", BF16, (M, H))
+    if ss is not None:
+        _check(ss, "ss", torch.float32, (M,))
+    _lib.call("ko_embed_ss", _lib.ptr(ids), _lib.ptr(emb), _lib.ptr(h), _lib.ptr(ss), M, H,
+              emb.shape[0], _lib.stream_ptr())
+
+
+def qk_norm_rope_acc(acc, q_w, k_w, cos, sin, pos, q_out, k_cache, v_cache, zero_buf, eps, nq,
+                     nkv, d):
+    """Decode (T=1) q/k norm + RoPE from the fp32 QKV accumulator (gemv.py:219-277):
+    rounds the projection to bf16, writes q and the K/V cache slot pos[b],
+    re-zeroes the consumed accumulator and zeroes ``zero_buf``."""
+    B = acc.shape[0]
+    _check(acc, "acc", torch.float32, (B, (nq + 2 * nkv) * d))
+    _check(q_out, "q_out", BF16, (B, nq * d))
+    _check(pos, "pos", torch.int32, (B,))
+    _check(q_w, "q_w", BF16, (d,))
+    _check(k_w, "k_w", BF16, (d,))
+    _check(cos, "cos", BF16)
+    _check(sin, "sin", BF16)
+    _need(k_cache.shape[0] == B and k_cache.stride(3) == 1 and k_cache.stride(2) == d,
+          "k_cache must be [B, nkv, cap, d] with sequence stride d")
+    _need(k_cache.stride() == v_cache.stride(), "k_cache and v_cache must share strides")
+    if zero_buf is not None:
+        _check(zero_buf, "zero_buf", torch.float32)
+    _lib.call("ko_qk_norm_rope_acc", _lib.ptr(acc), _lib.ptr(q_w), _lib.ptr(k_w), _lib.ptr(cos),
+              _lib.ptr(sin), _lib.ptr(pos), _lib.ptr(q_out), _lib.ptr(k_cache),
+              _lib.ptr(v_cache), _lib.ptr(zero_buf),
+              0 if zero_buf is None else zero_buf.numel(), B, k_cache.stride(0),
+              k_cache.stride(1), eps, nq, nkv, d, min(k_cache.shape[2], cos.shape[0], sin.shape[0]),
+              _lib.stream_ptr())

@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "koptim.h")
 def declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\bint\s+(ko_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(?:int|long long)\s+(ko_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")

@@ -1,0 +1,222 @@
+"""GPU parity of the fused decode ops and the GEMV family against the CPU oracle
+(engine/kernels/fused.py and gemv.py semantics). bf16 outputs are compared in
+bf16 units in the last place (ulp): the kernels follow the reference's cast
+chain, so only fp32 reduction order (and rsqrt/exp last-bit differences) may
+move a result by one bf16 ulp."""
+
+import pytest
+import torch
+
+from oracle import ops as O
+from tests.bf16util import assert_bf16_close, one_ulp_at
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def K():
+    from kernel_optim_amd.kernels import fused, gemv
+    return fused, gemv
+
+
+def _g(dev, seed):
+    return torch.Generator(device=dev).manual_seed(seed)
+
+
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_add_rms_norm(dev, with_delta):
+    fused, _ = K()
+    g = _g(dev, 1)
+    res = torch.randn(5, 2560, device=dev, generator=g).to(BF)
+    delta = torch.randn(5, 2560, device=dev, generator=g).to(BF) if with_delta else None
+    w = (1 + 0.1 * torch.randn(2560, device=dev, generator=g)).to(BF)
+    want_res, want = O.add_rms_norm(res.cpu(), None if delta is None else delta.cpu(), w.cpu(), 1e-6)
+    out = torch.empty_like(res)
+    fused.add_rms_norm(res, delta, w, out, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), want_res)
+    assert_bf16_close(out.cpu(), want)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_qk_norm_rope_append(dev, T):
+    fused, _ = K()
+    B, nq, nkv, d, cap = 3, 32, 8, 128, 96
+    g = _g(dev, 2)
+    qkv = torch.randn(B * T, (nq + 2 * nkv) * d, device=dev, generator=g).to(BF)
+    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(BF)
+    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(BF)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
+    pos = torch.tensor([0, 41, cap - T], dtype=torch.int32, device=dev)
+    kc = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(BF)
+    vc = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(BF)
+    kc0, vc0 = kc.cpu(), vc.cpu()
+    q_out = torch.empty(B * T, nq * d, device=dev, dtype=BF)
+    fused.qk_norm_rope(qkv, qw, kw, cos, sin, pos, q_out, kc, vc, T, 1e-6, nq, nkv, d)
+    torch.cuda.synchronize()
+    kref, vref = kc0.clone(), vc0.clone()
+    qref = O.qk_norm_rope(qkv.cpu(), qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), pos.cpu(), kref,
+                          vref, T, 1e-6, nq, nkv, d)
+    assert_bf16_close(q_out.cpu(), qref)
+    assert_bf16_close(kc.cpu(), kref, max_frac=1e-3)
+    assert torch.equal(vc.cpu(), vref)
+
+
+def test_qk_norm_rope_acc_rezeroes(dev):
+    _, gemv = K()
+    B, nq, nkv, d, cap = 2, 32, 8, 128, 40
+    g = _g(dev, 3)
+    acc = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g)
+    acc_cpu = acc.cpu()
+    qw = torch.ones(d, device=dev, dtype=BF)
+    kw = torch.ones(d, device=dev, dtype=BF)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap))
+    pos = torch.tensor([7, 39], dtype=torch.int32, device=dev)
+    kc = torch.zeros(B, nkv, cap, d, device=dev, dtype=BF)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(B, nq * d, device=dev, dtype=BF)
+    zb = torch.ones(2, B, device=dev)
+    gemv.qk_norm_rope_acc(acc, qw, kw, cos, sin, pos, q_out, kc, vc, zb, 1e-6, nq, nkv, d)
+    torch.cuda.synchronize()
+    assert torch.all(acc == 0) and torch.all(zb == 0)
+    kref, vref = torch.zeros(B, nkv, cap, d, dtype=BF), torch.zeros(B, nkv, cap, d, dtype=BF)
+    qref = O.qk_norm_rope_acc(acc_cpu, qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), pos.cpu(), kref,
+                              vref, 1e-6, nq, nkv, d)
+    assert_bf16_close(q_out.cpu(), qref)
+    assert_bf16_close(kc.cpu(), kref, max_frac=1e-3)
+    assert torch.equal(vc.cpu(), vref)
+
+
+def test_silu_mul(dev):
+    fused, _ = K()
+    g = _g(dev, 4)
+    gu = (3 * torch.randn(4, 2 * 9728, device=dev, generator=g)).to(BF)
+    out = torch.empty(4, 9728, device=dev, dtype=BF)
+    fused.silu_mul(gu, out)
+    torch.cuda.synchronize()
+    assert_bf16_close(out.cpu(), O.silu_mul(gu.cpu()))
+
+
+def test_embed_ss(dev):
+    _, gemv = K()
+    g = _g(dev, 5)
+    emb = torch.randn(151936, 2560, device=dev, generator=g).to(BF)
+    ids = torch.tensor([0, 151935, 4242, 7], device=dev)
+    h = torch.empty(4, 2560, device=dev, dtype=BF)
+    ss = torch.empty(4, device=dev)
+    gemv.embed_ss(ids, emb, h, ss)
+    torch.cuda.synchronize()
+    hr, ssr = O.embed_ss(ids.cpu(), emb.cpu())
+    assert torch.equal(h.cpu(), hr)
+    torch.testing.assert_close(ss.cpu(), ssr, rtol=1e-5, atol=1e-3)
+
+
+SHAPES = {  # Qwen3-4B decode projections (engine.py:258-264)
+    "qkv": (6144, 2560),
+    "o": (2560, 4096),
+    "gu": (9728, 2560),
+    "down": (2560, 9728),
+}
+
+
+def _weights(dev, N, K, seed, rows=None):
+    g = _g(dev, seed)
+    return (0.02 * torch.randn(rows or N, K, device=dev, generator=g)).to(BF)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 16])
+@pytest.mark.parametrize("rows", [4, 8])
+def test_gemv_epilogues(dev, M, rows):
+    _, gemv = K()
+    g = _g(dev, 10 + M)
+    # qkv: NORM + F32, ss computed in-kernel and passed explicitly
+    N, Kd = SHAPES["qkv"]
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    nw = (1 + 0.1 * torch.randn(Kd, device=dev, generator=g)).to(BF)
+    W = _weights(dev, N, Kd, 20)
+    ss = x.float().pow(2).sum(-1)
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32, nw=nw.cpu(), ss=ss.cpu())
+    for ss_arg in (None, ss):
+        y = torch.empty(M, N, device=dev)
+        gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)(x, W, y=y, nw=nw, ss=ss_arg, cfg=(rows,))
+        torch.cuda.synchronize()
+        torch.testing.assert_close(y.cpu(), want, rtol=2e-3, atol=2e-3)
+    # o: RESID with ss_out
+    N, Kd = SHAPES["o"]
+    a = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 21)
+    h = torch.randn(M, N, device=dev, generator=g).to(BF)
+    hr, ssr = O.gemv(a.cpu(), W.cpu(), O.EPI_RESID, h=h.cpu())
+    ss_out = torch.full((M,), 5.0, device=dev)
+    gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)(a, W, h=h, ss_out=ss_out, cfg=(rows,))
+    torch.cuda.synchronize()
+    assert_bf16_close(h.cpu(), hr, max_frac=0.02, atol=one_ulp_at(hr))
+    torch.testing.assert_close(ss_out.cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
+    # gu: NORM + SWIGLU
+    N, Kd = SHAPES["gu"]
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 22, rows=2 * N)
+    y = torch.empty(M, N, device=dev, dtype=BF)
+    gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)(x, W, y=y, nw=nw, cfg=(rows,))
+    torch.cuda.synchronize()
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_SWIGLU, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+    assert_bf16_close(y.cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
+    # down: BF16 (plain projection)
+    N, Kd = SHAPES["down"]
+    a = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 23)
+    y = torch.empty(M, N, device=dev, dtype=BF)
+    gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)(a, W, y=y, cfg=(rows,))
+    torch.cuda.synchronize()
+    want = O.gemv(a.cpu(), W.cpu(), O.EPI_BF16)
+    assert_bf16_close(y.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lm_head_argmax_and_graph_replay(dev, M):
+    _, gemv = K()
+    V, H = 151936, 2560
+    g = _g(dev, 30)
+    E = _weights(dev, V, H, 31)
+    x = torch.randn(M, H, device=dev, generator=g).to(BF)
+    nw = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(BF)
+    op = gemv.Gemv(M, V, H, gemv.EPI_ARGMAX, norm=True)
+    logits = torch.empty(M, V, device=dev, dtype=BF)
+    ids = torch.empty(M, device=dev, dtype=torch.int64)
+    op(x, E, y=logits, nw=nw, ids=ids)
+    torch.cuda.synchronize()
+    # self-consistent: ids is the first maximum of the kernel's own bf16 logits
+    assert torch.equal(ids.cpu(), O.argmax_first(logits.cpu()))
+    # close to the oracle, and the chosen logit is the oracle's maximum within 1 ulp
+    want = O.gemv(x.cpu(), E.cpu(), O.EPI_BF16, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+    assert_bf16_close(logits.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
+    wmax = want.float().max(-1).values
+    picked = want.float().gather(1, ids.cpu()[:, None])[:, 0]
+    assert torch.all(wmax - picked <= wmax.abs() * 2 ** -7)
+    # graph replays reuse the cross-workgroup counter
+    g2 = torch.cuda.CUDAGraph()
+    ids2 = torch.zeros_like(ids)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op(x, E, nw=nw, ids=ids2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g2):
+        op(x, E, nw=nw, ids=ids2)
+    for _ in range(3):
+        ids2.zero_()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids2, ids)
+
+
+def test_gemv_rejects_bad_shapes(dev):
+    _, gemv = K()
+    op = gemv.Gemv(1, 64, 128, gemv.EPI_BF16, norm=False)
+    x = torch.zeros(1, 128, device=dev, dtype=BF)
+    w = torch.zeros(64, 128, device=dev, dtype=BF)
+    with pytest.raises(ValueError):
+        op(x, w, y=torch.zeros(1, 64, device=dev))          # wrong dtype
+    with pytest.raises(ValueError):
+        op(x, w[:32], y=torch.zeros(1, 64, device=dev, dtype=BF))
