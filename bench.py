@@ -12,6 +12,9 @@ Prints one JSON line: value = algorithmic HBM GB/s (K+V of every valid key +
 q + out) over the timed steps; ``roofline`` for the dominant kernel
 (attn_partial_kernel) timed with HIP events on its launch stream;
 ``cpu_baseline`` = the CPU oracle on a bounded sample of the same workload.
+``decode_b1`` = the metric's second half: Qwen3-4B-architecture greedy decode
+tok/s at batch 1 (prompt 1024, 256 new tokens) against the weight-streaming
+roofline, with its own CPU baseline.
 """
 
 import argparse
@@ -30,8 +33,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the B1 decode measurement")
+    ap.add_argument("--no-attn", action="store_true",
+                    help="skip the attention measurement (profiling the decode step alone)")
+    ap.add_argument("--prompt", type=int, default=1024)
+    ap.add_argument("--new-tokens", type=int, default=256)
     return ap.parse_args()
 
 
@@ -70,19 +78,85 @@ def cpu_baseline(seconds):
     }
 
 
-def main():
-    args = parse_args()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode "
-              "attention path is built and measured per GPU, see DESIGN.md for sharding.",
-              file=sys.stderr)
-        sys.exit(2)
+def bench_decode(args):
+    """Qwen3-4B architecture (36 layers, random N(0,0.02) bf16 weights, seed 0),
+    B=1, prompt of seeded uniform-random ids, greedy decode of ``new_tokens``
+    through Engine.generate (hipGraph step, pipelined replays). tok/s counts the
+    decode steps after the first token (which comes from the prefill)."""
+    import torch
+    from kernel_optim_amd.engine import Engine
+    eng = Engine("random")
+    cfg = eng.cfg
+    S, N = args.prompt, args.new_tokens
+    prompt = torch.randint(0, cfg.vocab, (1, S), generator=torch.Generator().manual_seed(0)).tolist()
+    for _ in eng.generate(prompt, N):      # setup, tuning, capture, warm-up
+        pass
+    torch.cuda.synchronize()
+    t0 = None
+    out = []
+    for i, toks in enumerate(eng.generate(prompt, N)):
+        if i == 0:
+            t0 = time.perf_counter()
+        out.append(toks[0])
+    el = time.perf_counter() - t0
+    tok_s = (N - 1) / el
+    step_ms = eng.time_step(min(50, N - 1))
+    kv_per_key = cfg.layers * 2 * cfg.nkv * cfg.head_dim * 2
+    avg_keys = S + 1 + (N - 2) / 2.0            # keys read by decode steps 1..N-1
+    step_bytes = cfg.weight_bytes_per_step() + kv_per_key * avg_keys + kv_per_key
+    roof_tok_s = PEAK_HBM_GBS * 1e9 / step_bytes
+    res = {
+        "workload": f"Qwen3-4B architecture greedy decode, B=1, prompt {S}, {N} new tokens, "
+                    "random-init bf16 weights (seed 0), hipGraph decode step",
+        "tok_s": round(tok_s, 2),
+        "ms_per_token": round(1e3 / tok_s, 4),
+        "graph_step_ms": round(step_ms, 4),
+        "bytes_per_step": int(step_bytes),
+        "roofline": {"bound": "hbm", "tok_s_at_peak": round(roof_tok_s, 1),
+                     "frac": round(tok_s / roof_tok_s, 4),
+                     "achieved_gbs": round(step_bytes / (1e3 / tok_s) / 1e6, 1),
+                     "graph_step_frac": round((step_bytes / (step_ms * 1e-3) / 1e9) / PEAK_HBM_GBS, 4)},
+        "first_tokens": out[:8],
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
+    return res
+
+
+def cpu_decode_baseline(eng, seconds):
+    """The oracle's eager Qwen3 forward on the host CPU with the same weights:
+    prefill a 16-token prompt, then time single-token decode steps for about
+    ``seconds`` (weight streaming dominates a decode step, so the short context
+    understates the CPU's per-token cost only slightly)."""
+    import torch
+    from kernel_optim_amd.model import weights_to
+    from oracle.qwen3 import Qwen3Oracle
+    w = weights_to(eng.w, "cpu")
+    n_max = 64
+    orc = Qwen3Oracle(eng.cfg, w, B=1, cap=16 + n_max)
+    prompt = torch.randint(0, eng.cfg.vocab, (1, 16), generator=torch.Generator().manual_seed(0))
+    logits = orc.forward(prompt, 0)[:, -1]
+    tok = logits.float().argmax(-1)
+    n, t0 = 0, time.perf_counter()
+    while n < n_max - 1:
+        logits = orc.forward(tok[:, None], 16 + n)[:, -1]
+        tok = logits.float().argmax(-1)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(n / el, 4), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle.qwen3.Qwen3Oracle (bf16 F.linear, fp32 attention) on the CPU, same "
+                      f"36-layer weights, B=1, 16-token prompt, {n} decode steps in {el:.1f} s"}
+
+
+def bench_attention(args):
     import torch
     from kernel_optim_amd import _lib
     from kernel_optim_amd.kernels.fused import DecodeAttention
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     nbuf = 3
     gens = [torch.Generator(device=dev).manual_seed(s) for s in range(2 * nbuf + 1)]
     q = torch.randn(B, NQ * D, device=dev, generator=gens[0]).to(torch.bfloat16)
@@ -129,6 +203,7 @@ def main():
     torch.cuda.synchronize()
     k_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     k_gbs = nbytes / (k_ms * 1e-3) / 1e9
+    del ks, vs
 
     # ---- measured copy bandwidth for reference ----
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -143,35 +218,42 @@ def main():
     torch.cuda.synchronize()
     copy_gbs = 2 * src.numel() * 5 / (c0.elapsed_time(c1) * 1e-3) / 1e9
     del src, dst
-
-    line = {
-        "metric": METRIC,
+    torch.cuda.empty_cache()
+    return {
         "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
         "config": {"workload": "split-K GQA decode attention, B16 x 8192 ctx, 32q/8kv, d128, "
                                "bf16 contiguous KV cache, partial + LSE combine",
                    "batch": B, "ctx": CTX, "q_heads": NQ, "kv_heads": NKV, "head_dim": D,
                    "unit_keys": att.unit, "grid_waves": att.grid_waves},
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "wall_s_timed": round(wall, 4),
-        "roofline": {"bound": "hbm", "kernel": "attn_partial_kernel<1>",
+        "roofline": {"bound": "hbm", "kernel": "attn_kernel<1, false, false> (split-K partials)",
                      "achieved": round(k_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "avg_kernel_us": round(k_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": nbytes},
         "measured_copy_gbs": round(copy_gbs, 1),
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the decode path "
+              "is built and measured on one GPU's share of the work.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    torch.cuda.set_device(0)
+    line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+    if not args.no_attn:
+        line.update(bench_attention(args))
+        if not args.no_cpu:
+            line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if not args.no_decode:
+        line["decode_b1"] = bench_decode(args)
     print(json.dumps(line), flush=True)
 
 

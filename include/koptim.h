@@ -45,11 +45,33 @@ int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_l
                            int len_offset, int cap, int B, int T, int nq, int head_dim,
                            int unit, int max_units, void* out, void* stream);
 
-/* Both passes: the whole of DecodeAttention.__call__ (fused.py:221-234). */
+/* The whole of DecodeAttention.__call__ (fused.py:221-234). With counters == NULL:
+ * ko_decode_attn_partial followed by ko_decode_attn_combine, the reference's
+ * two launches. With counters ([B*nkv] int32, zero before the first call;
+ * every call leaves them zero) it is one launch: the last work unit of each
+ * (sequence, KV head) merges that pair's partials after a device-scope fence
+ * per unit. */
 int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens,
                    int len_offset, int cap, long long cache_b_stride, long long cache_h_stride,
                    int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,
-                   float scale, float* o_part, float* ml, void* out, void* stream);
+                   float scale, float* o_part, float* ml, int* counters, void* out,
+                   void* stream);
+
+/* One decode step of attention straight from the bf16 QKV projection
+ * qkv [B, (nq+2nkv)*head_dim] (T = 1): per-head q/k RMSNorm (gains q_w, k_w,
+ * eps) and RoPE (cos/sin [max_pos, head_dim] bf16) at position pos[b], append
+ * of k and v to cache slot pos[b], attention over keys 0..pos[b], and the
+ * combine into out [B, nq*head_dim] (a second launch, or the fused last-unit
+ * merge when counters != NULL, as for ko_decode_attn). Replaces the pair
+ * qk_norm_rope (engine/kernels/fused.py:54-106) + DecodeAttention.__call__
+ * (fused.py:221-234) as the reference's decode step calls them
+ * (engine/engine.py:328-330). Positions must lie in [0, min(cap, max_pos)). */
+int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const void* cos,
+                       const void* sin, int max_pos, const int* pos, void* k_cache,
+                       void* v_cache, int cap, long long cache_b_stride,
+                       long long cache_h_stride, int B, int nkv, int head_dim, int unit,
+                       int max_units, int grid_waves, float eps, float scale, float* o_part,
+                       float* ml, int* counters, void* out, void* stream);
 
 /* ---- residual add + RMSNorm ---------------------------------------------
  * Replaces engine/kernels/fused.py:16-36 (_add_rms_norm_kernel) as launched by
@@ -106,16 +128,22 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *     3 SWIGLU w [2N, K] (gate | up); y bf16 = bf16(bf16(silu(bf16 g)) * bf16 u)
  *     4 ARGMAX ids[m] (int64) = argmax_n bf16(acc) with lowest index on ties
  *              (torch.argmax at engine/engine.py:291, fused into the LM head);
- *              bf16 logits stored in y when y != NULL; part/counter are
- *              scratch (ko_gemv_argmax_scratch floats, one int zeroed once).
- * rows_per_wg: 4 or 8 output columns per 256-thread workgroup. K % 8 == 0. */
+ *              bf16 logits stored in y when y != NULL; pos_inc[m] += 1 when
+ *              pos_inc != NULL (the step's position advance, engine.py:292);
+ *              part: fp32 scratch of part_len >= ko_gemv_argmax_scratch(...).
+ * layout 0: each 256-thread workgroup owns `rows` (4 or 8) columns; any M.
+ * layout 1: each wavefront owns `rows` (1, 2, 4) columns, `waves` (2, 4)
+ *           wavefronts per workgroup; M <= 4 per launch slice.
+ * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
-            float* ss_out, long long* ids, float* part, int* counter, int M, int N, int K,
-            int epi, int norm, int accumulate, int rows_per_wg, float eps, void* stream);
+            float* ss_out, long long* ids, int* pos_inc, float* part, long long part_len, int M,
+            int N, int K, int epi, int norm, int accumulate, int layout, int rows, int waves,
+            float eps, void* stream);
 
-/* Number of fp32 scratch elements EPI 4 needs for N columns (a size, not a
- * status; -1 for bad arguments). Helper of ko_gemv, no reference counterpart. */
-long long ko_gemv_argmax_scratch(int N, int rows_per_wg);
+/* Number of fp32 scratch elements epi 4 (ARGMAX) needs for N columns with this
+ * launch configuration (a size, not a status; -1 for bad arguments). Helper of
+ * ko_gemv, no reference counterpart. */
+long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
 
 #ifdef __cplusplus
 }

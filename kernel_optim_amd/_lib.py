@@ -25,7 +25,11 @@ SIGNATURES = {
                                _int, _int, _int, _c_void_p, _c_void_p],
     "ko_decode_attn": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll, _int,
                        _int, _int, _int, _int, _int, _int, _f, _c_void_p, _c_void_p, _c_void_p,
-                       _c_void_p],
+                       _c_void_p, _c_void_p],
+    "ko_decode_attn_qkv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int,
+                           _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll, _int, _int, _int,
+                           _int, _int, _int, _f, _f, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                           _c_void_p],
     "ko_add_rms_norm": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _f, _c_void_p],
     "ko_qk_norm_rope": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                         _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll, _f, _int, _int,
@@ -36,9 +40,9 @@ SIGNATURES = {
     "ko_silu_mul": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
     "ko_embed_ss": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _c_void_p],
     "ko_gemv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _int, _int, _int, _int, _f,
-                _c_void_p],
-    "ko_gemv_argmax_scratch": [_int, _int],
+                _c_void_p, _c_void_p, _c_void_p, _ll, _int, _int, _int, _int, _int, _int, _int,
+                _int, _int, _f, _c_void_p],
+    "ko_gemv_argmax_scratch": [_int, _int, _int, _int],
 }
 
 # Entry points whose return value is a size, not a status.

@@ -1,12 +1,11 @@
-// Split-K GQA decode attention for gfx950 (MI355X), with the log-sum-exp
-// combine as a second pass.
+// Split-K GQA decode attention for gfx950 (MI355X).
 //
 // Replaces engine/kernels/fused.py:138-234 (_decode_attn_kernel,
 // _decode_combine_kernel, DecodeAttention.__call__). Semantics follow that
 // code: T query tokens per sequence at positions kv_len-T .. kv_len-1, causal
 // among themselves (query t sees keys < kv_len-T+t+1), softmax scale 1/sqrt(D),
 // query head h reads KV head h/4, P rounded to bf16 before the PV product,
-// fp32 partials (m, l, acc) merged by a log-sum-exp pass and rounded to bf16.
+// fp32 partials (m, l, acc) merged by a log-sum-exp combine, rounded to bf16.
 //
 // Work decomposition (length-aware, graph-safe): a "unit" is (b, kv_head,
 // c) covering keys [c*U, min((c+1)*U, kv_len_b)). Units are enumerated on the
@@ -24,6 +23,17 @@
 //   P    : rounded to bf16 and exchanged through 128*T bytes of LDS.
 //   PV   : v_dot2c_f32_bf16 over key pairs; each lane owns 8 head-dim columns
 //          of 4 keys per step, so V is read with fully coalesced 1 KiB loads.
+//
+// Variants (template flags):
+//   QKV   : the unit builds its q itself from the bf16 QKV projection (per-head
+//           RMSNorm + RoPE, engine/kernels/fused.py:71-87), and the unit that
+//           owns the new key position also norms/ropes k, appends k and v to
+//           the cache and uses them from registers (the work of
+//           qk_norm_rope, fused.py:54-96, folded in; decode T = 1).
+//   FUSED : the last unit of each (b, kv_head) to finish (per-pair arrival
+//           counter) merges the pair's partials and writes the bf16 output,
+//           so no second launch is needed; it re-arms the counter for the
+//           next launch.
 #include "ko_common.h"
 
 using namespace ko;
@@ -35,6 +45,28 @@ constexpr int G = 4;            // query heads per KV head
 constexpr int WAVES = 4;        // wavefronts per workgroup
 constexpr float TAU = 8.0f;     // lazy-rescale threshold, log2 units
 constexpr float NEG_BIG = -1.0e30f;
+
+struct AttnArgs {
+  const uint16_t* q;     // [B*T, nq*D] (unless QKV)
+  const uint16_t* qkv;   // [B, (nq+2nkv)*D] (QKV)
+  const uint16_t* qw;    // [D] q_norm gain (QKV)
+  const uint16_t* kw;    // [D] k_norm gain (QKV)
+  const uint16_t* cosb;  // [rows, D] (QKV)
+  const uint16_t* sinb;
+  float eps;
+  int max_pos;           // rows of the RoPE tables (QKV)
+  uint16_t* kc;
+  uint16_t* vc;
+  const int* lens;
+  int len_off, cap;
+  long long cb, ch;
+  int B, nkv, unit, max_units;
+  float scale_log2;
+  float* o_part;
+  float* ml;
+  int* counters;         // [B*nkv] (FUSED)
+  uint16_t* out;         // [B*T, nq*D] (FUSED)
+};
 
 __device__ __forceinline__ int nunits(int len, int unit) {
   return len > 0 ? (len + unit - 1) / unit : 0;
@@ -79,47 +111,202 @@ __device__ void locate_pair(int p, const int* lens, int off, int cap, int B, int
   c_out = 0;
 }
 
-template <int T>
-__global__ __launch_bounds__(256) void attn_partial_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int* __restrict__ lens, int len_off, int cap,
-    long long cb, long long ch, int B, int nkv, int unit, int max_units, float scale_log2,
-    float* __restrict__ o_part, float* __restrict__ ml) {
+// Per-head RMSNorm + RoPE of one head held in the MFMA operand layout: lane
+// (r, g) holds head-dim elements 32i+8g .. +7 for i = 0..3, and the four lanes
+// r, r+16, r+32, r+48 together hold the whole head. The rotate_half partner of
+// element d (d +- 64) is i +- 2 in the same lane.
+__device__ __forceinline__ void norm_rope_head(const uint4 (&x)[4], const uint4 (&w)[4],
+                                               const uint4 (&c)[4], const uint4 (&s)[4],
+                                               float eps, uint4 (&y)[4]) {
+  float xf[4][8], wf[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+    const uint32_t wv[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xf[i][2 * e] = bf16lo(xv[e]);
+      xf[i][2 * e + 1] = bf16hi(xv[e]);
+      wf[i][2 * e] = bf16lo(wv[e]);
+      wf[i][2 * e + 1] = bf16hi(wv[e]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += xf[i][e] * xf[i][e];
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  const float rstd = rsqrtf(ss / (float)D + eps);
+  float xn[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xn[i][e] = round_bf16(wf[i][e] * round_bf16(xf[i][e] * rstd));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t cv[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+    const uint32_t sv[4] = {s[i].x, s[i].y, s[i].z, s[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float yy[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 2 * e + h;
+        const float rot = i < 2 ? -xn[i + 2][k] : xn[i - 2][k];
+        const float cf = h ? bf16hi(cv[e]) : bf16lo(cv[e]);
+        const float sf = h ? bf16hi(sv[e]) : bf16lo(sv[e]);
+        yy[h] = round_bf16(xn[i][k] * cf) + round_bf16(rot * sf);
+      }
+      o[e] = pack_bf16x2(yy[0], yy[1]);
+    }
+    y[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// Log-sum-exp merge of n unit partials of row R (one wavefront; lane owns
+// head-dim elements 2l, 2l+1), normalise, round to bf16. Latency-lean: lane c
+// loads (m_c, l_c) for all units at once and computes the unit weight
+// w_c = 2^(m_c - M); the partial accumulators are then loaded 16 units at a
+// time with no dependence between the loads of a batch.
+__device__ void combine_row(const float* __restrict__ o_part, const float* __restrict__ ml,
+                            long long R, int n, int max_units, uint16_t* __restrict__ out) {
+  const int lane = lane_id();
+  const float2* mlr = reinterpret_cast<const float2*>(ml) + R * max_units;
+  const float* op = o_part + R * max_units * D + 2 * lane;
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  float M = NEG_BIG;
+  for (int c = lane; c < n; c += 64) M = fmaxf(M, mlr[c].x);
+  M = wave_max(M);
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    const int c = c0 + lane;
+    float wl = 0.f, w = 0.f;
+    if (c < n) {
+      const float2 mlc = mlr[c];
+      w = __builtin_amdgcn_exp2f(mlc.x - M);
+      wl = w * mlc.y;
+    }
+    L += wave_sum(wl);
+    const int cn = min(64, n - c0);
+    for (int j0 = 0; j0 < cn; j0 += 16) {
+      float2 a16[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (j0 + j < cn) a16[j] = *reinterpret_cast<const float2*>(op + (long long)(c0 + j0 + j) * D);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (j0 + j < cn) {
+          const float wj = __shfl(w, j0 + j, 64);
+          o0 += wj * a16[j].x;
+          o1 += wj * a16[j].y;
+        }
+      }
+    }
+  }
+  const float r0 = L > 0.f ? o0 / L : 0.f;
+  const float r1 = L > 0.f ? o1 / L : 0.f;
+  reinterpret_cast<uint32_t*>(out + R * D)[lane] = pack_bf16x2(r0, r1);
+}
+
+template <int T, bool QKV, bool FUSED>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  static_assert(!QKV || T == 1, "the QKV prologue serves one decode token per sequence");
   __shared__ __align__(16) uint16_t lds_p[WAVES][T][G][16];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;   // key slot of the QK lanes / column chunk of the PV lanes
   const int g = lane >> 4;   // MFMA k-group / PV key row
-  const int nq = nkv * G;
+  const int nkv = a.nkv, nq = nkv * G, unit = a.unit, max_units = a.max_units;
   const int W = gridDim.x * WAVES;
-  const int total = count_pairs(lens, len_off, cap, B, unit) * nkv;
+  const int total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
   uint16_t* myp = &lds_p[wave][0][0][0];
 
   for (int u = blockIdx.x * WAVES + wave; u < total; u += W) {
     const int pidx = u / nkv;
     const int kvh = u - pidx * nkv;
     int b, c;
-    locate_pair(pidx, lens, len_off, cap, B, unit, b, c);
+    locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
     b = uniform(b);
     c = uniform(c);
     if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
-    const int kv_len = uniform(seq_len(lens, b, len_off, cap));
+    const int kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
     const int k0 = c * unit;
     const int k1 = min(k0 + unit, kv_len);
-    const uint16_t* kb = kc + (long long)b * cb + (long long)kvh * ch;
-    const uint16_t* vb = vc + (long long)b * cb + (long long)kvh * ch;
+    const uint16_t* kb = a.kc + (long long)b * a.cb + (long long)kvh * a.ch;
+    const uint16_t* vb = a.vc + (long long)b * a.cb + (long long)kvh * a.ch;
 
-    // Q as the MFMA A operand: row r -> (token (r/4)%T, head r%4); lane group
-    // g supplies head-dim elements 32i+8g .. 32i+8g+7 for MFMA i.
+    // ---- K/V loads of a 16-key step (clamped to the unit's last key) ----
+    auto load_k = [&](int kk, uint4* kr) {
+      const int key = min(kk + r, k1 - 1);
+      const uint16_t* p = kb + (long long)key * D + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[i] = ldg16_stream(p + 32 * i);
+    };
+    auto load_v = [&](int kk, uint4* vr) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key = min(kk + g + 4 * s, k1 - 1);
+        vr[s] = ldg16_stream(vb + (long long)key * D + 8 * r);
+      }
+    };
+    uint4 ka[4], va[4], kb2[4], vb2[4];
+    load_k(k0, ka);
+    load_v(k0, va);
+
+    // ---- Q as the MFMA A operand: row r -> (token (r/4)%T, head r%4); lane
+    // group g supplies head-dim elements 32i+8g .. 32i+8g+7 for MFMA i ----
     bf16x8 qa[4];
-    {
+    const int pnew = kv_len - 1;                     // QKV: position of the new key
+    const bool has_new = QKV && k0 <= pnew && pnew < k1;
+    uint4 knew[4], vnew;
+    if constexpr (QKV) {
+      const int nqkv = (nq + 2 * nkv) * D;
+      const int pt = min(max(pnew, 0), a.max_pos - 1);
+      const uint16_t* src = a.qkv + (long long)b * nqkv;
+      uint4 xq[4], wq[4], cs[4], sn[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * i + 8 * g;
+        xq[i] = ldg16(src + (kvh * G + (r & 3)) * D + d);
+        wq[i] = ldg16(a.qw + d);
+        cs[i] = ldg16(a.cosb + (long long)pt * D + d);
+        sn[i] = ldg16(a.sinb + (long long)pt * D + d);
+      }
+      uint4 qn[4];
+      norm_rope_head(xq, wq, cs, sn, a.eps, qn);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, qn[i]);
+      if (has_new) {
+        uint4 xk[4], wk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * i + 8 * g;
+          xk[i] = ldg16(src + (nq + kvh) * D + d);
+          wk[i] = ldg16(a.kw + d);
+        }
+        norm_rope_head(xk, wk, cs, sn, a.eps, knew);
+        vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
+        // KV append at slot pnew (fused.py:88-96): k by the r == 0 lanes,
+        // v by the g == 0 lanes.
+        uint16_t* kdst = a.kc + (long long)b * a.cb + (long long)kvh * a.ch + (long long)pnew * D;
+        uint16_t* vdst = a.vc + (long long)b * a.cb + (long long)kvh * a.ch + (long long)pnew * D;
+        if (r == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(kdst + 32 * i + 8 * g) = knew[i];
+        }
+        if (g == 0) *reinterpret_cast<uint4*>(vdst + 8 * r) = vnew;
+      }
+    } else {
       const int trow = (r >> 2) % T;
       const uint16_t* qrow =
-          q + ((long long)(b * T + trow) * nq + kvh * G + (r & 3)) * D + 8 * g;
+          a.q + ((long long)(b * T + trow) * nq + kvh * G + (r & 3)) * D + 8 * g;
 #pragma unroll
       for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, ldg16(qrow + 32 * i));
     }
+
     const int tq = g % T;                           // token of this lane's score rows
     const int lim = min(k1, kv_len - T + tq + 1);   // exclusive causal key limit
 
@@ -137,21 +324,20 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
 #pragma unroll
     for (int j = 0; j < G; ++j) lsum[j] = 0.f;
 
-    auto load_k = [&](int kk, uint4* kr) {
-      const int key = min(kk + r, k1 - 1);
-      const uint16_t* p = kb + (long long)key * D + 8 * g;
+    auto step = [&](int kk, const uint4* kr_in, const uint4* vr_in) {
+      uint4 kr[4], vr[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = ldg16_stream(p + 32 * i);
-    };
-    auto load_v = [&](int kk, uint4* vr) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int key = min(kk + g + 4 * s, k1 - 1);
-        vr[s] = ldg16_stream(vb + (long long)key * D + 8 * r);
+      for (int i = 0; i < 4; ++i) {
+        kr[i] = kr_in[i];
+        vr[i] = vr_in[i];
       }
-    };
-
-    auto step = [&](int kk, const uint4* kr, const uint4* vr) {
+      if (has_new && kk <= pnew && pnew < kk + 16) {  // the new key: use registers
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (r == pnew - kk) kr[i] = knew[i];
+          if (kk + g + 4 * i == pnew) vr[i] = vnew;
+        }
+      }
       f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -161,7 +347,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
       float s[G], mrow[G];
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        s[j] = valid ? sc[j] * scale_log2 : -INFINITY;
+        s[j] = valid ? sc[j] * a.scale_log2 : -INFINITY;
         float m = mu[0][j];
 #pragma unroll
         for (int t = 1; t < T; ++t) m = (tq == t) ? mu[t][j] : m;
@@ -187,13 +373,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
           }
 #pragma unroll
         for (int j = 0; j < G; ++j) {
-          float a = alpha[0][j], m = mu[0][j];
+          float al = alpha[0][j], m = mu[0][j];
 #pragma unroll
           for (int t = 1; t < T; ++t) {
-            a = (tq == t) ? alpha[t][j] : a;
+            al = (tq == t) ? alpha[t][j] : al;
             m = (tq == t) ? mu[t][j] : m;
           }
-          lsum[j] *= a;
+          lsum[j] *= al;
           mrow[j] = m;
         }
       }
@@ -248,9 +434,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     };
 
     // Two-deep software pipeline over 16-key steps.
-    uint4 ka[4], va[4], kb2[4], vb2[4];
-    load_k(k0, ka);
-    load_v(k0, va);
     for (int kk = k0; kk < k1; kk += 32) {
       load_k(kk + 16, kb2);
       load_v(kk + 16, vb2);
@@ -279,7 +462,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const long long R = (long long)(b * T + t) * nq + kvh * G + g;
-      float* dst = o_part + (R * max_units + c) * D + 8 * r;
+      float* dst = a.o_part + (R * max_units + c) * D + 8 * r;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         if (g == j) {
@@ -300,55 +483,97 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
           l = (r == j) ? lrow[j] : l;
         }
       const long long R = (long long)(b * T + g) * nq + kvh * G + r;
-      reinterpret_cast<float2*>(ml)[R * max_units + c] = make_float2(m, l);
+      reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(m, l);
+    }
+
+    if constexpr (FUSED) {
+      // Publish this unit's partials, count its arrival; the last arrival of
+      // the (b, kv_head) pair merges the pair's partials.
+      __threadfence();
+      int prev = 0;
+      int* ctr = a.counters + (long long)b * nkv + kvh;
+      if (lane == 0) prev = atomicAdd(ctr, 1);
+      prev = readlane(prev, 0);
+      const int n = nunits(kv_len, unit);
+      if (prev == n - 1) {
+        __threadfence();
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int j = 0; j < G; ++j)
+            combine_row(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, max_units,
+                        a.out);
+        if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
 
-// One wavefront per output row (b, t, q_head): log-sum-exp merge of the
-// unit partials, normalise, round to bf16.
+// Second pass when no counters are given: one wavefront per output row.
 __global__ __launch_bounds__(256) void attn_combine_kernel(
     const float* __restrict__ o_part, const float* __restrict__ ml,
     const int* __restrict__ lens, int len_off, int cap, int T, int nq, int rows, int unit,
     int max_units, uint16_t* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
   const int R = blockIdx.x * WAVES + (threadIdx.x >> 6);
   if (R >= rows) return;
   const int b = R / (T * nq);
   const int n = nunits(seq_len(lens, b, len_off, cap), unit);
-  const float2* mlr = reinterpret_cast<const float2*>(ml) + (long long)R * max_units;
-  float M = NEG_BIG;
-  for (int c = lane; c < n; c += 64) M = fmaxf(M, mlr[c].x);
-  M = wave_max(M);
-  float L = 0.f, o0 = 0.f, o1 = 0.f;
-  const float* op = o_part + (long long)R * max_units * D + 2 * lane;
-  for (int c = 0; c < n; ++c) {
-    const float2 mlc = mlr[c];
-    const float w = __builtin_amdgcn_exp2f(mlc.x - M);
-    L += w * mlc.y;
-    const float2 a = *reinterpret_cast<const float2*>(op + (long long)c * D);
-    o0 += w * a.x;
-    o1 += w * a.y;
-  }
-  const float r0 = L > 0.f ? o0 / L : 0.f;
-  const float r1 = L > 0.f ? o1 / L : 0.f;
-  reinterpret_cast<uint32_t*>(out + (long long)R * D)[lane] = pack_bf16x2(r0, r1);
+  combine_row(o_part, ml, R, n, max_units, out);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_attn_args(const void* q, const void* kc, const void* vc, const int* lens, int cap,
-                    long long cb, long long ch, int B, int T, int nkv, int head_dim, int unit,
-                    int max_units, const float* o_part, const float* ml) {
-  if (!q || !kc || !vc || !lens || !o_part || !ml) return KO_EINVAL;
+int check_common(const void* kc, const void* vc, const int* lens, int cap, long long cb,
+                 long long ch, int B, int T, int nkv, int head_dim, int unit, int max_units,
+                 const float* o_part, const float* ml) {
+  if (!kc || !vc || !lens || !o_part || !ml) return KO_EINVAL;
   if (head_dim != D) return KO_ENOTSUP;
   if (T < 1 || T > 4) return KO_ENOTSUP;
   if (B < 1 || nkv < 1 || cap < 1) return KO_EINVAL;
   if (unit < 16 || (unit & 15)) return KO_EINVAL;
   if ((long long)max_units * unit < cap) return KO_ERANGE;
-  if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(o_part)) return KO_EINVAL;
+  if (!aligned16(kc) || !aligned16(vc) || !aligned16(o_part)) return KO_EINVAL;
   if ((cb & 7) || (ch & 7) || cb < 0 || ch < 0) return KO_EINVAL;
   return KO_OK;
+}
+
+template <int T, bool QKV, bool FUSED>
+int launch(const AttnArgs& a, int grid_waves, hipStream_t s) {
+  const dim3 grid((grid_waves + WAVES - 1) / WAVES), block(64 * WAVES);
+  hipLaunchKernelGGL((attn_kernel<T, QKV, FUSED>), grid, block, 0, s, a);
+  return KO_LAUNCH_STATUS();
+}
+
+template <bool FUSED>
+int launch_t(const AttnArgs& a, int T, int grid_waves, hipStream_t s) {
+  switch (T) {
+    case 1: return launch<1, false, FUSED>(a, grid_waves, s);
+    case 2: return launch<2, false, FUSED>(a, grid_waves, s);
+    case 3: return launch<3, false, FUSED>(a, grid_waves, s);
+    default: return launch<4, false, FUSED>(a, grid_waves, s);
+  }
+}
+
+AttnArgs base_args(const void* k_cache, const void* v_cache, const int* lens, int len_offset,
+                   int cap, long long cb, long long ch, int B, int nkv, int unit, int max_units,
+                   float scale, float* o_part, float* ml) {
+  AttnArgs a = {};
+  a.kc = static_cast<uint16_t*>(const_cast<void*>(k_cache));
+  a.vc = static_cast<uint16_t*>(const_cast<void*>(v_cache));
+  a.lens = lens;
+  a.len_off = len_offset;
+  a.cap = cap;
+  a.cb = cb;
+  a.ch = ch;
+  a.B = B;
+  a.nkv = nkv;
+  a.unit = unit;
+  a.max_units = max_units;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.o_part = o_part;
+  a.ml = ml;
+  a.max_pos = 1;
+  return a;
 }
 
 }  // namespace
@@ -360,28 +585,14 @@ int ko_decode_attn_partial(const void* q, const void* k_cache, const void* v_cac
                            long long cache_b_stride, long long cache_h_stride, int B, int T,
                            int nkv, int head_dim, int unit, int max_units, int grid_waves,
                            float scale, float* o_part, float* ml, void* stream) {
-  int st = check_attn_args(q, k_cache, v_cache, kv_lens, cap, cache_b_stride, cache_h_stride,
-                           B, T, nkv, head_dim, unit, max_units, o_part, ml);
+  int st = check_common(k_cache, v_cache, kv_lens, cap, cache_b_stride, cache_h_stride, B, T, nkv,
+                        head_dim, unit, max_units, o_part, ml);
   if (st) return st;
-  if (grid_waves < 1) return KO_EINVAL;
-  const dim3 grid((grid_waves + WAVES - 1) / WAVES), block(64 * WAVES);
-  const float sl2 = scale * 1.4426950408889634f;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint16_t* qq = static_cast<const uint16_t*>(q);
-  const uint16_t* kk = static_cast<const uint16_t*>(k_cache);
-  const uint16_t* vv = static_cast<const uint16_t*>(v_cache);
-#define KO_ATTN_LAUNCH(TT)                                                                   \
-  hipLaunchKernelGGL(attn_partial_kernel<TT>, grid, block, 0, s, qq, kk, vv, kv_lens,        \
-                     len_offset, cap, cache_b_stride, cache_h_stride, B, nkv, unit, max_units, \
-                     sl2, o_part, ml)
-  switch (T) {
-    case 1: KO_ATTN_LAUNCH(1); break;
-    case 2: KO_ATTN_LAUNCH(2); break;
-    case 3: KO_ATTN_LAUNCH(3); break;
-    default: KO_ATTN_LAUNCH(4); break;
-  }
-#undef KO_ATTN_LAUNCH
-  return KO_LAUNCH_STATUS();
+  if (!q || !aligned16(q) || grid_waves < 1) return KO_EINVAL;
+  AttnArgs a = base_args(k_cache, v_cache, kv_lens, len_offset, cap, cache_b_stride,
+                         cache_h_stride, B, nkv, unit, max_units, scale, o_part, ml);
+  a.q = static_cast<const uint16_t*>(q);
+  return launch_t<false>(a, T, grid_waves, static_cast<hipStream_t>(stream));
 }
 
 int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_lens,
@@ -401,13 +612,59 @@ int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_l
 int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens,
                    int len_offset, int cap, long long cache_b_stride, long long cache_h_stride,
                    int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,
-                   float scale, float* o_part, float* ml, void* out, void* stream) {
-  int st = ko_decode_attn_partial(q, k_cache, v_cache, kv_lens, len_offset, cap, cache_b_stride,
-                                  cache_h_stride, B, T, nkv, head_dim, unit, max_units,
-                                  grid_waves, scale, o_part, ml, stream);
+                   float scale, float* o_part, float* ml, int* counters, void* out,
+                   void* stream) {
+  if (!counters) {
+    int st = ko_decode_attn_partial(q, k_cache, v_cache, kv_lens, len_offset, cap,
+                                    cache_b_stride, cache_h_stride, B, T, nkv, head_dim, unit,
+                                    max_units, grid_waves, scale, o_part, ml, stream);
+    if (st) return st;
+    return ko_decode_attn_combine(o_part, ml, kv_lens, len_offset, cap, B, T, nkv * G, head_dim,
+                                  unit, max_units, out, stream);
+  }
+  int st = check_common(k_cache, v_cache, kv_lens, cap, cache_b_stride, cache_h_stride, B, T, nkv,
+                        head_dim, unit, max_units, o_part, ml);
   if (st) return st;
-  return ko_decode_attn_combine(o_part, ml, kv_lens, len_offset, cap, B, T, nkv * G, head_dim,
-                                unit, max_units, out, stream);
+  if (!q || !aligned16(q) || !out || !aligned16(out) || grid_waves < 1) return KO_EINVAL;
+  AttnArgs a = base_args(k_cache, v_cache, kv_lens, len_offset, cap, cache_b_stride,
+                         cache_h_stride, B, nkv, unit, max_units, scale, o_part, ml);
+  a.q = static_cast<const uint16_t*>(q);
+  a.counters = counters;
+  a.out = static_cast<uint16_t*>(out);
+  return launch_t<true>(a, T, grid_waves, static_cast<hipStream_t>(stream));
+}
+
+int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const void* cos,
+                       const void* sin, int max_pos, const int* pos, void* k_cache,
+                       void* v_cache, int cap, long long cache_b_stride,
+                       long long cache_h_stride, int B, int nkv, int head_dim, int unit,
+                       int max_units, int grid_waves, float eps, float scale, float* o_part,
+                       float* ml, int* counters, void* out, void* stream) {
+  int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
+                        head_dim, unit, max_units, o_part, ml);
+  if (st) return st;
+  if (!qkv || !q_w || !k_w || !cos || !sin || !out || max_pos < 1 || grid_waves < 1)
+    return KO_EINVAL;
+  if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
+      !aligned16(sin) || !aligned16(out))
+    return KO_EINVAL;
+  AttnArgs a = base_args(k_cache, v_cache, pos, 1, cap, cache_b_stride, cache_h_stride, B, nkv,
+                         unit, max_units, scale, o_part, ml);
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.qw = static_cast<const uint16_t*>(q_w);
+  a.kw = static_cast<const uint16_t*>(k_w);
+  a.cosb = static_cast<const uint16_t*>(cos);
+  a.sinb = static_cast<const uint16_t*>(sin);
+  a.eps = eps;
+  a.max_pos = max_pos;
+  a.counters = counters;
+  a.out = static_cast<uint16_t*>(out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (counters) return launch<1, true, true>(a, grid_waves, s);
+  st = launch<1, true, false>(a, grid_waves, s);
+  if (st) return st;
+  return ko_decode_attn_combine(o_part, ml, pos, 1, cap, B, 1, nkv * G, head_dim, unit,
+                                max_units, out, stream);
 }
 
 }  // extern "C"

@@ -1,5 +1,5 @@
 // Fused skinny GEMM ("GEMV") for the decode step on gfx950:
-//   y[M, N] = x[M, K] @ W[N, K]^T, M <= 16 rows per launch, each weight read once.
+//   y[M, N] = x[M, K] @ W[N, K]^T, each weight read once for all M rows.
 //
 // Replaces engine/kernels/gemv.py:30-150 (_gemv_kernel, Gemv.__call__) with the
 // same prologue/epilogue semantics (gemv.py:7-18, 86-106):
@@ -10,15 +10,21 @@
 //   BF16   : y = bf16(acc)
 //   RESID  : h <- bf16(h + bf16(acc)); ss_out[m] += sum_n h_new^2 (when given)
 //   SWIGLU : W is [2N, K] = gate | up; y = bf16(bf16(silu(bf16 g)) * bf16 u)
-//   ARGMAX : BF16 logits (stored when y != NULL) and ids[m] = argmax_n bf16(acc),
-//            lowest index on ties (torch.argmax, engine.py:291), reduced across
-//            workgroups by the last one to finish.
+//   ARGMAX : bf16 logits (stored when y != NULL) and ids[m] = argmax_n bf16(acc),
+//            lowest index on ties (torch.argmax, engine.py:291). Each work unit
+//            writes its best (value, index) to scratch; a one-workgroup-per-row
+//            finalize kernel reduces them in index order (no cross-workgroup
+//            atomics) and optionally advances the decode positions.
 //
-// Mapping: a 256-thread workgroup owns R output columns (2R weight rows for
-// SWIGLU) over the full K. Thread t reads the 16-byte chunks t, t+256, ... of
-// each row (coalesced 4 KiB per row per step), two steps in flight, and keeps
-// M x R fp32 partial dots (v_dot2c_f32_bf16); partials are reduced with DPP
-// row sums and 1 KiB of LDS. HBM traffic is the weights once; x comes from L2.
+// Two mappings of rows to the machine (both stream each weight row with
+// coalesced 16-byte loads and accumulate with v_dot2c_f32_bf16):
+//   layout 0 "block": a 256-thread workgroup owns R output columns over the
+//            full K; thread t reads chunks t, t+256, ...; M <= 16.
+//   layout 1 "wave" : a wavefront owns RW output columns over the full K (lane l
+//            reads chunks l, l+64, ...); WPB wavefronts per workgroup share the
+//            normalised x through LDS, so the NORM prologue runs once per
+//            workgroup. Row counts are chosen so every CU gets the same number
+//            of rows (e.g. N=2560 -> 10 rows per CU). M <= 4.
 #include "ko_common.h"
 
 using namespace ko;
@@ -36,9 +42,8 @@ struct GemvArgs {
   const float* ss;
   uint16_t* h;
   float* ss_out;
-  long long* ids;
-  float2* part;
-  int* counter;
+  float2* part;  // ARGMAX: [M][nparts] (value, index bits)
+  int nparts;
   int mrows, N, K;
   float eps;
   int accumulate;
@@ -52,7 +57,7 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
   return c;
 }
 
-// bf16(nw * bf16(x * rstd)) on 8 packed elements (gemv.py:77-79).
+// bf16(nw * bf16(x * rstd)) on packed pairs (gemv.py:77-79).
 __device__ __forceinline__ uint32_t norm2(uint32_t x, uint32_t w, float rstd) {
   const float a = bf16lo(w) * round_bf16(bf16lo(x) * rstd);
   const float b = bf16hi(w) * round_bf16(bf16hi(x) * rstd);
@@ -73,14 +78,41 @@ __device__ __forceinline__ float sq8(const uint4& v) {
   return s;
 }
 
+// Epilogue for one finished output element (m, n) with full sums (tot, tot2).
+// Returns the bf16-rounded new residual squared (RESID) or 0.
+template <int EPI>
+__device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float tot, float tot2) {
+  const long long o = (long long)m * a.N + n;
+  if constexpr (EPI == EPI_F32) {
+    float* y = static_cast<float*>(a.y);
+    if (a.accumulate) atomicAdd(y + o, tot);
+    else y[o] = tot;
+  } else if constexpr (EPI == EPI_BF16) {
+    static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(tot);
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    const float g = round_bf16(tot), u = round_bf16(tot2);
+    const float s = round_bf16(g / (1.0f + expf(-g)));
+    static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(s * u);
+  } else if constexpr (EPI == EPI_RESID) {
+    const float hn = round_bf16(bf16_to_f32(a.h[o]) + round_bf16(tot));
+    a.h[o] = f32_to_bf16(hn);
+    return hn * hn;
+  } else {  // ARGMAX: logits only; the selection is done by the caller
+    if (a.y) static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(tot);
+  }
+  return 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// layout 0: 256-thread workgroup per R output columns
+// ---------------------------------------------------------------------------
 template <int M, int R, bool NORM, int EPI>
-__global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(NT) void gemv_block_kernel(GemvArgs a) {
   constexpr int NW = EPI == EPI_SWIGLU ? 2 * R : R;
   __shared__ float red[16][M * NW];
   __shared__ float s_rstd[M];
   __shared__ float s_h2[M * R];
   __shared__ float2 s_best[M * R];
-  __shared__ int s_last;
 
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int n0 = blockIdx.x * R;
@@ -171,7 +203,6 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // ---- reduce the partial dots over the 256 threads ----
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -190,34 +221,12 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
       if constexpr (EPI == EPI_SWIGLU) tot2 += red[i][m * NW + R + r];
     }
     const bool ok = m < mr && n < N;
-    const long long o = (long long)m * N + n;
-    if constexpr (EPI == EPI_F32) {
-      if (ok) {
-        float* y = static_cast<float*>(a.y);
-        if (a.accumulate) atomicAdd(y + o, tot);
-        else y[o] = tot;
-      }
-    } else if constexpr (EPI == EPI_BF16) {
-      if (ok) static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(tot);
-    } else if constexpr (EPI == EPI_SWIGLU) {
-      if (ok) {
-        const float g = round_bf16(tot), u = round_bf16(tot2);
-        const float s = round_bf16(g / (1.0f + expf(-g)));
-        static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(s * u);
-      }
-    } else if constexpr (EPI == EPI_RESID) {
-      float hn2 = 0.f;
-      if (ok) {
-        const float hn = round_bf16(bf16_to_f32(a.h[o]) + round_bf16(tot));
-        a.h[o] = f32_to_bf16(hn);
-        hn2 = hn * hn;
-      }
-      s_h2[idx] = hn2;
-    } else {  // EPI_ARGMAX
-      const float v = round_bf16(tot);
-      if (ok && a.y) static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(tot);
-      s_best[idx] = make_float2(ok ? v : -INFINITY, __int_as_float(ok ? n : 0x7fffffff));
-    }
+    float h2 = 0.f;
+    if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+    if constexpr (EPI == EPI_RESID) s_h2[idx] = h2;
+    if constexpr (EPI == EPI_ARGMAX)
+      s_best[idx] = make_float2(ok ? round_bf16(tot) : -INFINITY,
+                                __int_as_float(ok ? n : 0x7fffffff));
   }
 
   if constexpr (EPI == EPI_RESID) {
@@ -231,69 +240,230 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
       }
     }
   }
-
   if constexpr (EPI == EPI_ARGMAX) {
     __syncthreads();
-    const int nwg = gridDim.x;
-    if (t == 0) {
-      for (int m = 0; m < mr; ++m) {
-        float2 best = s_best[m * R];
-        for (int r = 1; r < R; ++r) {
-          const float2 c = s_best[m * R + r];
-          if (c.x > best.x) best = c;  // columns ascend with r: ties keep the lower index
-        }
-        a.part[(long long)m * nwg + blockIdx.x] = best;
+    if (t < M && t < mr) {
+      float2 best = s_best[t * R];
+      for (int r = 1; r < R; ++r) {
+        const float2 c = s_best[t * R + r];
+        if (c.x > best.x) best = c;  // columns ascend with r: ties keep the lower index
       }
-      __threadfence();
-      const int prev = atomicAdd(a.counter, 1);
-      s_last = prev == nwg - 1;
-    }
-    __syncthreads();
-    if (s_last) {
-      __threadfence();
-      for (int m = 0; m < mr; ++m) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int i = t; i < nwg; i += NT) {
-          const float2 c = a.part[(long long)m * nwg + i];
-          const int ci = __float_as_int(c.y);
-          if (c.x > bv || (c.x == bv && ci < bi)) {
-            bv = c.x;
-            bi = ci;
-          }
-        }
-        // workgroup argmax with lowest-index tie break
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-          const float ov = __shfl_xor(bv, off, 64);
-          const int oi = __shfl_xor(bi, off, 64);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        if (lane == 0) s_best[wv] = make_float2(bv, __int_as_float(bi));
-        __syncthreads();
-        if (t == 0) {
-          float2 best = s_best[0];
-          for (int i = 1; i < NT / 64; ++i) {
-            const float2 c = s_best[i];
-            if (c.x > best.x || (c.x == best.x && __float_as_int(c.y) < __float_as_int(best.y)))
-              best = c;
-          }
-          a.ids[m] = __float_as_int(best.y);
-        }
-        __syncthreads();
-      }
-      if (t == 0) *a.counter = 0;  // ready for the next launch (graph replays)
+      a.part[(long long)t * a.nparts + blockIdx.x] = best;
     }
   }
 }
 
+// ---------------------------------------------------------------------------
+// layout 1: one wavefront per RW output columns, WPB wavefronts per workgroup
+// ---------------------------------------------------------------------------
+constexpr int LDS_X_BYTES = 40960;  // normalised x staged for the workgroup (M*K*2)
+
+template <int M, int RW, int WPB, bool NORM, int EPI>
+__global__ __launch_bounds__(64 * WPB) void gemv_wave_kernel(GemvArgs a) {
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 * RW : RW;
+  constexpr int UNR = 4;  // chunks per lane in flight per row
+  __shared__ __align__(16) uint16_t s_x[NORM ? LDS_X_BYTES / 2 : 8];
+  __shared__ float s_red[WPB][M];
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int N = a.N, K = a.K, KC = K >> 3, mr = a.mrows;
+  const int unit = blockIdx.x * WPB + wv;   // this wave's row group
+  const int n0 = unit * RW;
+
+  const uint16_t* wp[NW];
+#pragma unroll
+  for (int r = 0; r < NW; ++r) {
+    const int n = r < RW ? min(n0 + r, N - 1) : N + min(n0 + r - RW, N - 1);
+    wp[r] = a.w + (long long)n * K;
+  }
+
+  // First weight chunks do not depend on the prologue.
+  uint4 wcur[UNR][NW];
+#pragma unroll
+  for (int u = 0; u < UNR; ++u) {
+    const int c = lane + 64 * u;
+    if (c < KC) {
+#pragma unroll
+      for (int r = 0; r < NW; ++r) wcur[u][r] = ldg16_stream(wp[r] + 8 * c);
+    }
+  }
+
+  const uint16_t* xsrc = a.x;
+  if constexpr (NORM) {
+    // rstd per row, then the normalised x into LDS, shared by the WPB waves.
+    float rstd[M];
+    if (a.ss) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) rstd[m] = m < mr ? rsqrtf(a.ss[m] / (float)K + a.eps) : 0.f;
+    } else {
+      float sq[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) sq[m] = 0.f;
+      for (int c = threadIdx.x; c < KC; c += 64 * WPB) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          if (m < mr) sq[m] += sq8(ldg16(a.x + (long long)m * K + 8 * c));
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float v = wave_sum(sq[m]);
+        if (lane == 0) s_red[wv][m] = v;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < WPB; ++i) s += s_red[i][m];
+        rstd[m] = rsqrtf(s / (float)K + a.eps);
+      }
+    }
+    for (int c = threadIdx.x; c < KC; c += 64 * WPB) {
+      const uint4 nwv = ldg16(a.nw + 8 * c);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint4 xv = m < mr ? ldg16(a.x + (long long)m * K + 8 * c) : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(s_x + (long long)m * K + 8 * c) = norm8(xv, nwv, rstd[m]);
+      }
+    }
+    __syncthreads();
+  }
+
+  if (n0 >= N) return;  // a trailing wave with no rows (after the shared prologue)
+
+  float acc[M][NW];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < NW; ++r) acc[m][r] = 0.f;
+
+  for (int cb = 0; cb < KC; cb += 64 * UNR) {
+    uint4 wnext[UNR][NW];
+    const bool more = cb + 64 * UNR < KC;
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int c = cb + 64 * UNR + lane + 64 * u;
+        if (c < KC) {
+#pragma unroll
+          for (int r = 0; r < NW; ++r) wnext[u][r] = ldg16_stream(wp[r] + 8 * c);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = cb + lane + 64 * u;
+      if (c < KC) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          if (m < mr) {
+            uint4 xv;
+            if constexpr (NORM) xv = *reinterpret_cast<const uint4*>(s_x + (long long)m * K + 8 * c);
+            else xv = ldg16(xsrc + (long long)m * K + 8 * c);
+#pragma unroll
+            for (int r = 0; r < NW; ++r) acc[m][r] = dot8(xv, wcur[u][r], acc[m][r]);
+          }
+        }
+      }
+    }
+    if (!more) break;
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+#pragma unroll
+      for (int r = 0; r < NW; ++r) wcur[u][r] = wnext[u][r];
+  }
+
+  // Reduce each (m, r) partial over the 64 lanes; every lane ends with the sums.
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < NW; ++r) acc[m][r] = wave_sum(acc[m][r]);
+
+  // Each output element is finished by one lane (lane (m*RW + r) % 64).
+  float h2[M];
+  float2 best[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    h2[m] = 0.f;
+    best[m] = make_float2(-INFINITY, __int_as_float(0x7fffffff));
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = n0 + r;
+      const bool ok = m < mr && n < N;
+      if (ok && lane == ((m * RW + r) & 63))
+        h2[m] += epilogue<EPI>(a, m, n, acc[m][r], EPI == EPI_SWIGLU ? acc[m][NW - RW + r] : 0.f);
+      if constexpr (EPI == EPI_ARGMAX) {
+        const float v = round_bf16(acc[m][r]);
+        if (ok && v > best[m].x) best[m] = make_float2(v, __int_as_float(n));  // ties keep lower n
+      }
+    }
+  if constexpr (EPI == EPI_RESID) {
+    if (a.ss_out) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float s = wave_sum(h2[m]);
+        if (m < mr && lane == 0) atomicAdd(a.ss_out + m, s);
+      }
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        if (m < mr) a.part[(long long)m * a.nparts + unit] = best[m];
+    }
+  }
+}
+
+// One workgroup per row m: argmax over the work units' (value, index) pairs,
+// lowest index on ties; optionally pos[m] += 1 (the decode step's position
+// advance, engine.py:292).
+__global__ __launch_bounds__(NT) void argmax_finalize_kernel(const float2* __restrict__ part,
+                                                             int nparts, long long* __restrict__ ids,
+                                                             int* __restrict__ pos) {
+  __shared__ float2 s_best[NT / 64];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = t; i < nparts; i += NT) {
+    const float2 c = part[(long long)m * nparts + i];
+    const int ci = __float_as_int(c.y);
+    if (c.x > bv || (c.x == bv && ci < bi)) {
+      bv = c.x;
+      bi = ci;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) s_best[wv] = make_float2(bv, __int_as_float(bi));
+  __syncthreads();
+  if (t == 0) {
+    float2 best = s_best[0];
+    for (int i = 1; i < NT / 64; ++i) {
+      const float2 c = s_best[i];
+      if (c.x > best.x || (c.x == best.x && __float_as_int(c.y) < __float_as_int(best.y)))
+        best = c;
+    }
+    ids[m] = __float_as_int(best.y);
+    if (pos) pos[m] += 1;
+  }
+}
+
 template <int M, int R>
-int launch_m(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+int launch_block(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
   const dim3 grid((a.N + R - 1) / R), block(NT);
-#define KO_G(NORMV, EPIV) hipLaunchKernelGGL((gemv_kernel<M, R, NORMV, EPIV>), grid, block, 0, s, a)
+#define KO_G(NORMV, EPIV) \
+  hipLaunchKernelGGL((gemv_block_kernel<M, R, NORMV, EPIV>), grid, block, 0, s, a)
   switch (epi) {
     case EPI_F32: if (norm) KO_G(true, EPI_F32); else KO_G(false, EPI_F32); break;
     case EPI_BF16: if (norm) KO_G(true, EPI_BF16); else KO_G(false, EPI_BF16); break;
@@ -306,36 +476,88 @@ int launch_m(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
 }
 
 template <int R>
-int launch_r(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
-  if (a.mrows <= 1) return launch_m<1, R>(a, epi, norm, s);
-  if (a.mrows <= 2) return launch_m<2, R>(a, epi, norm, s);
-  if (a.mrows <= 4) return launch_m<4, R>(a, epi, norm, s);
-  if (a.mrows <= 8) return launch_m<8, R>(a, epi, norm, s);
-  return launch_m<16, R>(a, epi, norm, s);
+int launch_block_r(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  if (a.mrows <= 1) return launch_block<1, R>(a, epi, norm, s);
+  if (a.mrows <= 2) return launch_block<2, R>(a, epi, norm, s);
+  if (a.mrows <= 4) return launch_block<4, R>(a, epi, norm, s);
+  if (a.mrows <= 8) return launch_block<8, R>(a, epi, norm, s);
+  return launch_block<16, R>(a, epi, norm, s);
+}
+
+template <int M, int RW, int WPB>
+int launch_wave(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  const int units = (a.N + RW - 1) / RW;
+  const dim3 grid((units + WPB - 1) / WPB), block(64 * WPB);
+#define KO_W(NORMV, EPIV) \
+  hipLaunchKernelGGL((gemv_wave_kernel<M, RW, WPB, NORMV, EPIV>), grid, block, 0, s, a)
+  switch (epi) {
+    case EPI_F32: if (norm) KO_W(true, EPI_F32); else KO_W(false, EPI_F32); break;
+    case EPI_BF16: if (norm) KO_W(true, EPI_BF16); else KO_W(false, EPI_BF16); break;
+    case EPI_RESID: if (norm) KO_W(true, EPI_RESID); else KO_W(false, EPI_RESID); break;
+    case EPI_SWIGLU: if (norm) KO_W(true, EPI_SWIGLU); else KO_W(false, EPI_SWIGLU); break;
+    default: if (norm) KO_W(true, EPI_ARGMAX); else KO_W(false, EPI_ARGMAX); break;
+  }
+#undef KO_W
+  return KO_LAUNCH_STATUS();
+}
+
+template <int RW, int WPB>
+int launch_wave_m(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  if (a.mrows <= 1) return launch_wave<1, RW, WPB>(a, epi, norm, s);
+  if (a.mrows <= 2) return launch_wave<2, RW, WPB>(a, epi, norm, s);
+  return launch_wave<4, RW, WPB>(a, epi, norm, s);
+}
+
+int launch_wave_cfg(const GemvArgs& a, int epi, bool norm, int rw, int wpb, hipStream_t s) {
+  if (rw == 1 && wpb == 2) return launch_wave_m<1, 2>(a, epi, norm, s);
+  if (rw == 1 && wpb == 4) return launch_wave_m<1, 4>(a, epi, norm, s);
+  if (rw == 2 && wpb == 2) return launch_wave_m<2, 2>(a, epi, norm, s);
+  if (rw == 2 && wpb == 4) return launch_wave_m<2, 4>(a, epi, norm, s);
+  if (rw == 4 && wpb == 2) return launch_wave_m<4, 2>(a, epi, norm, s);
+  if (rw == 4 && wpb == 4) return launch_wave_m<4, 4>(a, epi, norm, s);
+  return KO_ENOTSUP;
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+long long parts_for(int N, int layout, int rows, int waves) {
+  if (layout == 0) return (N + rows - 1) / rows;
+  const long long units = (N + rows - 1) / rows;
+  return ((units + waves - 1) / waves) * waves;
+}
 
 }  // namespace
 
 extern "C" {
 
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
-            float* ss_out, long long* ids, float* part, int* counter, int M, int N, int K,
-            int epi, int norm, int accumulate, int rows_per_wg, float eps, void* stream) {
+            float* ss_out, long long* ids, int* pos_inc, float* part, long long part_len, int M,
+            int N, int K, int epi, int norm, int accumulate, int layout, int rows, int waves,
+            float eps, void* stream) {
   if (!x || !w || M < 1 || N < 1 || K < 8 || (K & 7)) return KO_EINVAL;
   if (epi < EPI_F32 || epi > EPI_ARGMAX) return KO_EINVAL;
   if (!al16(x) || !al16(w)) return KO_EINVAL;
   if (norm && (!nw || !al16(nw))) return KO_EINVAL;
   if ((epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_SWIGLU) && !y) return KO_EINVAL;
   if (epi == EPI_RESID && !h) return KO_EINVAL;
-  if (epi == EPI_ARGMAX && (!ids || !part || !counter)) return KO_EINVAL;
-  if (rows_per_wg != 4 && rows_per_wg != 8) return KO_ENOTSUP;
+  if (layout == 0) {
+    if (rows != 4 && rows != 8) return KO_ENOTSUP;
+  } else if (layout == 1) {
+    if (M > 4) return KO_ENOTSUP;
+    if (norm && (long long)M * K * 2 > LDS_X_BYTES) return KO_ENOTSUP;
+  } else {
+    return KO_EINVAL;
+  }
+  const int mstep = layout == 0 ? 16 : 4;
+  const long long nparts = parts_for(N, layout, rows, waves);
+  if (epi == EPI_ARGMAX) {
+    if (!ids || !part) return KO_EINVAL;
+    if (part_len < 2LL * mstep * nparts) return KO_ERANGE;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Slices of at most 16 rows per launch.
-  for (int m0 = 0; m0 < M; m0 += 16) {
+  for (int m0 = 0; m0 < M; m0 += mstep) {
     GemvArgs a;
-    const int mr = M - m0 < 16 ? M - m0 : 16;
+    const int mr = M - m0 < mstep ? M - m0 : mstep;
     a.x = static_cast<const uint16_t*>(x) + (long long)m0 * K;
     a.w = static_cast<const uint16_t*>(w);
     a.y = nullptr;
@@ -347,26 +569,34 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
     a.ss = ss ? ss + m0 : nullptr;
     a.h = h ? static_cast<uint16_t*>(h) + (long long)m0 * N : nullptr;
     a.ss_out = ss_out ? ss_out + m0 : nullptr;
-    a.ids = ids ? ids + m0 : nullptr;
     a.part = reinterpret_cast<float2*>(part);
-    a.counter = counter;
+    a.nparts = (int)nparts;
     a.mrows = mr;
     a.N = N;
     a.K = K;
     a.eps = eps;
     a.accumulate = accumulate;
-    const int st = rows_per_wg == 4 ? launch_r<4>(a, epi, norm != 0, s)
-                                    : launch_r<8>(a, epi, norm != 0, s);
+    int st;
+    if (layout == 0)
+      st = rows == 4 ? launch_block_r<4>(a, epi, norm != 0, s) : launch_block_r<8>(a, epi, norm != 0, s);
+    else
+      st = launch_wave_cfg(a, epi, norm != 0, rows, waves, s);
     if (st) return st;
+    if (epi == EPI_ARGMAX) {
+      hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(NT), 0, s, a.part, a.nparts,
+                         ids + m0, pos_inc ? pos_inc + m0 : nullptr);
+      st = KO_LAUNCH_STATUS();
+      if (st) return st;
+    }
   }
   return KO_OK;
 }
 
-// Scratch floats needed by EPI_ARGMAX for N columns with rows_per_wg rows per
-// workgroup: 2 per (row, workgroup) for at most 16 rows per launch.
-long long ko_gemv_argmax_scratch(int N, int rows_per_wg) {
-  if (N < 1 || rows_per_wg < 1) return -1;
-  return 2LL * 16 * ((N + rows_per_wg - 1) / rows_per_wg);
+// fp32 scratch elements ko_gemv needs for EPI 4 (ARGMAX) with this layout
+// (a size, not a status; -1 for bad arguments).
+long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
+  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 1) return -1;
+  return 2LL * 16 * parts_for(N, layout, rows, waves);
 }
 
 }  // extern "C"

@@ -14,12 +14,14 @@ Per shape (B, S, N) the engine allocates a static KV cache
 [layers, B, 8, cap, 128] bf16, prefills the prompt with PyTorch-ROCm ops
 (kernel_optim_amd.prefill), and captures one decode step in a hipGraph
 (torch.cuda.CUDAGraph) that is replayed per token. The decode step is
-7 kernels per layer, all from libkoptim (engine.py:274-292):
-  qkv GEMV (RMSNorm prologue) -> q/k norm + RoPE + KV append ->
-  split-K attention (partial + LSE combine) -> o GEMV (+residual) ->
+5 kernels per layer, all from libkoptim (the reference's 7, engine.py:274-292,
+with the q/k norm + RoPE + KV append and the split-K combine folded into the
+attention launch):
+  qkv GEMV (RMSNorm prologue) -> attention (q/k norm + RoPE + KV append
+  prologue, split-K partials, last-unit LSE combine) -> o GEMV (+residual) ->
   gate/up GEMV (RMSNorm prologue, SwiGLU epilogue) -> down GEMV (+residual)
 and around the layers the embedding gather and the LM head with the greedy
-argmax fused into it. Replays are pipelined: the next step is queued before
+argmax fused into it (its finalize kernel also advances the positions). Replays are pipelined: the next step is queued before
 the host waits for the previous step's ids (engine.py:509-522).
 """
 
@@ -29,7 +31,7 @@ import time
 
 import torch
 
-from .kernels.fused import DecodeAttention, qk_norm_rope
+from .kernels.fused import DecodeAttention
 from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
@@ -137,7 +139,7 @@ class Engine:
             deadline = time.monotonic() + TUNE_BUDGET_S
             for name, (g, ws) in self.gv.items():
                 g.tune(ws, deadline)
-                _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us")
+                _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
         self.g1 = self._capture(self._step1)
         self._shape = key
 
@@ -149,15 +151,14 @@ class Engine:
         embed_ss(self.ids, self.w["embed"], h, None)
         for i, lw in enumerate(self.w["layers"]):
             g["qkv"](h, lw["qkv"], y=self.qkv, nw=lw["w_in"])
-            qk_norm_rope(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin, self.pos,
-                         self.q1, self.k_cache[i], self.v_cache[i], 1, cfg.eps, cfg.nq, cfg.nkv,
-                         cfg.head_dim)
-            self.attn(self.q1, self.k_cache[i], self.v_cache[i], self.pos, self.attn_out)
+            self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
+                                 self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
+                                 cfg.eps)
             g["o"](self.attn_out, lw["o"], h=h)
             g["gu"](h, lw["gu"], y=self.act, nw=lw["w_post"])
             g["down"](self.act, lw["down"], h=h)
-        g["lm"](h, self.w["lm_head"], y=self.logits, nw=self.w["final_norm"], ids=self.ids)
-        self.pos.add_(1)
+        g["lm"](h, self.w["lm_head"], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
+                pos_inc=self.pos)
 
     def _capture(self, fn):
         # Warm up on a side stream, then capture. Warm-up steps write cache slot 0,
@@ -186,10 +187,12 @@ class Engine:
         if self.logits is not None:
             self.logits.copy_(logits)
 
+    @torch.inference_mode()
     def step(self):
         """Replay one decode step (for callers that drive decoding themselves)."""
         self.g1.replay()
 
+    @torch.inference_mode()
     def time_step(self, reps=20):
         """Mean GPU time (ms) of one replayed decode step, from positions S."""
         torch.cuda.synchronize()

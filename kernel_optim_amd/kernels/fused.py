@@ -60,12 +60,17 @@ class DecodeAttention:
     only valid keys are read and short sequences take few units. A fixed grid
     of ``grid_waves`` wavefronts strides over the units (graph-safe).
     ``target_ctas`` is the number of wavefronts to fill the GPU with
-    (256 CUs x 8 by default).
+    (256 CUs x 8 by default). A second launch merges the partials, as the
+    reference does; with ``fused_combine`` the last unit of each (sequence, KV
+    head) merges them in the same launch instead, through an arrival counter
+    and a device-scope fence per unit (slower on MI355X, where that fence
+    writes back the L2, so it is off by default).
     """
 
     MAX_T = 4
 
-    def __init__(self, B, T, cap, nq, nkv, d, device, target_ctas=2048, unit=None):
+    def __init__(self, B, T, cap, nq, nkv, d, device, target_ctas=2048, unit=None,
+                 fused_combine=False):
         _need(d == 128, "head_dim must be 128")
         _need(nq == 4 * nkv, "the kernel serves GQA groups of 4 query heads per KV head")
         _need(1 <= T <= self.MAX_T, f"T must be in 1..{self.MAX_T}")
@@ -80,20 +85,28 @@ class DecodeAttention:
         rows = B * T * nq
         self.o_part = torch.empty(rows * self.max_units * d, dtype=torch.float32, device=device)
         self.ml = torch.empty(rows * self.max_units * 2, dtype=torch.float32, device=device)
+        # per-(sequence, KV head) arrival counters; every launch leaves them at zero
+        self.counters = (torch.zeros(B * nkv, dtype=torch.int32, device=device) if fused_combine
+                         else None)
         self.scale = d ** -0.5
+
+    def _check_kv(self, k_cache, v_cache, lens):
+        B, nkv, d, cap = self.B, self.nkv, self.d, self.cap
+        _check_cache(k_cache, "k_cache", B, nkv, cap, d)
+        _check_cache(v_cache, "v_cache", B, nkv, cap, d)
+        _need(k_cache.stride() == v_cache.stride(), "k_cache and v_cache must share strides")
+        _check(lens, "pos/lengths", torch.int32, (B,))
 
     def _run(self, q, k_cache, v_cache, lens, len_offset, out):
         B, T, nq, nkv, d, cap = self.B, self.T, self.nq, self.nkv, self.d, self.cap
         _check(q, "q", BF16, (B * T, nq * d))
         _check(out, "out", BF16, (B * T, nq * d))
-        _check_cache(k_cache, "k_cache", B, nkv, cap, d)
-        _check_cache(v_cache, "v_cache", B, nkv, cap, d)
-        _need(k_cache.stride() == v_cache.stride(), "k_cache and v_cache must share strides")
-        _check(lens, "pos/lengths", torch.int32, (B,))
+        self._check_kv(k_cache, v_cache, lens)
         _lib.call("ko_decode_attn", _lib.ptr(q), _lib.ptr(k_cache), _lib.ptr(v_cache),
                   _lib.ptr(lens), len_offset, cap, k_cache.stride(0), k_cache.stride(1),
                   B, T, nkv, d, self.unit, self.max_units, self.grid_waves, self.scale,
-                  _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(out), _lib.stream_ptr())
+                  _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters),
+                  _lib.ptr(out), _lib.stream_ptr())
 
     def __call__(self, q, k_cache, v_cache, pos, out):
         """q: [B*T, NQ*D]; k/v_cache: [B, NKV, cap, D]; pos: [B] int32 (first query
@@ -104,6 +117,29 @@ class DecodeAttention:
         """Ragged form: lengths[b] = number of valid keys of sequence b (int32);
         the T queries sit at positions lengths[b]-T .. lengths[b]-1."""
         self._run(q, k_cache, v_cache, lengths, 0, out)
+
+    def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps):
+        """Decode step (T=1) straight from the bf16 QKV projection [B, (nq+2nkv)*d]:
+        per-head q/k RMSNorm + RoPE at pos[b], append of k and v at slot pos[b], and
+        attention over keys 0..pos[b] -- qk_norm_rope (fused.py:54-96) and this
+        op's __call__ with the q/k work folded into the attention launch."""
+        B, nq, nkv, d = self.B, self.nq, self.nkv, self.d
+        _need(self.T == 1, "decode_qkv serves one decode token per sequence")
+        _check(qkv, "qkv", BF16, (B, (nq + 2 * nkv) * d))
+        _check(out, "out", BF16, (B, nq * d))
+        _check(q_w, "q_w", BF16, (d,))
+        _check(k_w, "k_w", BF16, (d,))
+        _check(cos, "cos", BF16)
+        _check(sin, "sin", BF16)
+        _need(cos.dim() == 2 and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape),
+              "cos/sin must be [rows, d]")
+        self._check_kv(k_cache, v_cache, pos)
+        _lib.call("ko_decode_attn_qkv", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w),
+                  _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], _lib.ptr(pos), _lib.ptr(k_cache),
+                  _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
+                  self.unit, self.max_units, self.grid_waves, eps, self.scale,
+                  _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters),
+                  _lib.ptr(out), _lib.stream_ptr())
 
 
 # ---------------------------------------------------------------------------

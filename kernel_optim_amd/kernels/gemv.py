@@ -16,9 +16,12 @@ Additions of this backend:
 - NORM with ``ss=None`` computes the row's sum of squares from x inside the
   kernel (no separate sum-of-squares buffer or zeroing discipline needed).
 
-``cfg`` is an opaque tuple ``(rows_per_workgroup,)``. ``allow_split`` is
-accepted for signature compatibility; this kernel never splits K (each
-workgroup streams full rows), so the F32 epilogue is a plain store.
+``cfg`` is an opaque tuple ``(layout, rows, waves)``: layout 0 gives each
+256-thread workgroup ``rows`` output columns (any M); layout 1 gives each
+wavefront ``rows`` columns with ``waves`` wavefronts per workgroup sharing the
+normalised input through LDS (M <= 4). ``allow_split`` is accepted for
+signature compatibility; the kernels never split K (each work unit streams
+full rows), so the F32 epilogue is a plain store.
 """
 
 import time
@@ -42,26 +45,31 @@ class Gemv:
         self.allow_split = allow_split
         self.cfg = self.candidates()[0]
         self._part = None
-        self._counter = None
         self.us = float("nan")
 
     def candidates(self):
-        """Rows per workgroup: 4 keeps more workgroups in flight for small N,
-        8 halves the per-workgroup norm prologue for large N."""
-        if self.epi == EPI_ARGMAX or self.N >= 32768:
-            return [(8,), (4,)]
-        return [(4,), (8,)]
+        """Launch configurations, the default first. Layout 1 (a wavefront per row
+        group) is the batch-1..4 path; layout 0 serves every batch up to 16 rows
+        per launch."""
+        out = []
+        if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):
+            per_wave = (4, 2, 1) if self.N >= 32768 else (1, 2, 4)
+            for rows in per_wave:
+                for waves in (2, 4):
+                    out.append((1, rows, waves))
+        out += [(0, 4, 0), (0, 8, 0)] if self.N < 32768 else [(0, 8, 0), (0, 4, 0)]
+        return out
 
-    def _scratch(self, device):
-        if self._part is None or self._part.device != device:
-            n = _lib.lib().ko_gemv_argmax_scratch(self.N, 4)
+    def _scratch(self, device, cfg):
+        n = _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg)
+        if self._part is None or self._part.device != device or self._part.numel() < n:
             self._part = torch.empty(max(n, 2), dtype=torch.float32, device=device)
-            self._counter = torch.zeros(1, dtype=torch.int32, device=device)
-        return self._part, self._counter
+        return self._part
 
-    def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None):
+    def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None,
+                 pos_inc=None):
         M, N, K, epi = self.M, self.N, self.K, self.epi
-        (rows,) = cfg or self.cfg
+        layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
         _check(w, "w", BF16, ((2 * N) if epi == EPI_SWIGLU else N, K))
         if self.norm:
@@ -80,13 +88,14 @@ class Gemv:
             _check(ids, "ids", torch.int64, (M,))
             if y is not None:
                 _check(y, "y", BF16, (M, N))
-        part = counter = None
-        if epi == EPI_ARGMAX:
-            part, counter = self._scratch(x.device)
+            if pos_inc is not None:
+                _check(pos_inc, "pos_inc", torch.int32, (M,))
+        part = self._scratch(x.device, (layout, rows, waves)) if epi == EPI_ARGMAX else None
         _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
                   _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
-                  _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(part), _lib.ptr(counter),
-                  M, N, K, epi, int(self.norm), 0, rows, self.eps, _lib.stream_ptr())
+                  _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(pos_inc), _lib.ptr(part),
+                  0 if part is None else part.numel(), M, N, K, epi, int(self.norm), 0, layout,
+                  rows, waves, self.eps, _lib.stream_ptr())
 
     def tune(self, weights, deadline):
         """Pick the fastest candidate by GPU time: one call per layer weight (cold),
@@ -100,6 +109,7 @@ class Gemv:
         ids = torch.zeros(M, device=dev, dtype=torch.int64)
         kw = dict(y=y, nw=nw, h=h, ids=ids)
         best = None
+        self.tune_log = []
         for cfg in self.candidates():
             if time.monotonic() > deadline:
                 break
@@ -122,6 +132,7 @@ class Gemv:
             except RuntimeError:
                 torch.cuda.synchronize()
                 continue
+            self.tune_log.append((cfg, round(t / (2 * len(weights)) * 1e3, 2)))
             if best is None or t < best[0]:
                 best = (t, cfg)
         if best is not None:

@@ -185,3 +185,55 @@ def test_bad_arguments_raise_before_launch(dev):
         att(q.float(), k, v, pos, torch.empty_like(q))
     with pytest.raises(ValueError):
         att(q, k[:, :, :32], v, pos, torch.empty_like(q))
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_two_launch_and_fused_combine_agree(dev, fused):
+    fused_mod = _fused()
+    B, cap = 5, 700
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(19, 20, 21))
+    pos = torch.tensor([699, 0, 63, 64, 350], dtype=torch.int32, device=dev)
+    att = fused_mod.DecodeAttention(B, 1, cap, 32, 8, 128, dev, unit=64, fused_combine=fused)
+    out = torch.empty_like(q)
+    for _ in range(3):  # counters must re-arm between launches
+        att(q, k, v, pos, out)
+        torch.cuda.synchronize()
+        want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [int(p) + 1 for p in pos])
+        torch.testing.assert_close(out.cpu().double(), want, **TOL)
+    if fused:
+        assert torch.all(att.counters == 0)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("B,cap,unit", [(1, 1300, 64), (4, 600, 128), (16, 256, 64)])
+def test_decode_qkv_matches_norm_rope_append_then_attention(dev, B, cap, unit, fused):
+    """decode_qkv = qk_norm_rope (fused.py:54-96) then attention over keys 0..pos."""
+    from oracle import ops as O
+    fused_mod = _fused()
+    nq, nkv, d = 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(40 + B)
+    qkv = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
+    k = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, cap, (B,), device=dev, generator=g).to(torch.int32)
+    pos[0] = cap - 1
+    if B > 1:
+        pos[1] = 0
+    kref, vref = k.cpu(), v.cpu()
+    qref = O.qk_norm_rope(qkv.cpu(), qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), pos.cpu(), kref,
+                          vref, 1, 1e-6, nq, nkv, d)
+    want = A.decode_attention(qref, kref, vref, [int(p) + 1 for p in pos])
+    att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, unit=unit, fused_combine=fused)
+    out = torch.empty(B, nq * d, device=dev, dtype=torch.bfloat16)
+    att.decode_qkv(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6)
+    if fused:
+        assert torch.all(att.counters == 0)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().double(), want, **TOL)
+    # the appended slot holds the normed+roped k and the raw v; nothing else changed
+    from tests.bf16util import assert_bf16_close
+    assert_bf16_close(k.cpu(), kref, max_frac=1e-3)
+    assert torch.equal(v.cpu(), vref)

@@ -124,10 +124,16 @@ def _weights(dev, N, K, seed, rows=None):
     return (0.02 * torch.randn(rows or N, K, device=dev, generator=g)).to(BF)
 
 
+CFGS = [(0, 4, 0), (0, 8, 0), (1, 1, 2), (1, 2, 4), (1, 4, 2)]
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 16])
-@pytest.mark.parametrize("rows", [4, 8])
-def test_gemv_epilogues(dev, M, rows):
+@pytest.mark.parametrize("cfg", CFGS)
+def test_gemv_epilogues(dev, M, cfg):
     _, gemv = K()
+    if cfg[0] == 1 and M > 4:
+        pytest.skip("layout 1 serves M <= 4")
+    rows = cfg
     g = _g(dev, 10 + M)
     # qkv: NORM + F32, ss computed in-kernel and passed explicitly
     N, Kd = SHAPES["qkv"]
@@ -138,7 +144,7 @@ def test_gemv_epilogues(dev, M, rows):
     want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32, nw=nw.cpu(), ss=ss.cpu())
     for ss_arg in (None, ss):
         y = torch.empty(M, N, device=dev)
-        gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)(x, W, y=y, nw=nw, ss=ss_arg, cfg=(rows,))
+        gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)(x, W, y=y, nw=nw, ss=ss_arg, cfg=rows)
         torch.cuda.synchronize()
         torch.testing.assert_close(y.cpu(), want, rtol=2e-3, atol=2e-3)
     # o: RESID with ss_out
@@ -148,7 +154,7 @@ def test_gemv_epilogues(dev, M, rows):
     h = torch.randn(M, N, device=dev, generator=g).to(BF)
     hr, ssr = O.gemv(a.cpu(), W.cpu(), O.EPI_RESID, h=h.cpu())
     ss_out = torch.full((M,), 5.0, device=dev)
-    gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)(a, W, h=h, ss_out=ss_out, cfg=(rows,))
+    gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)(a, W, h=h, ss_out=ss_out, cfg=rows)
     torch.cuda.synchronize()
     assert_bf16_close(h.cpu(), hr, max_frac=0.02, atol=one_ulp_at(hr))
     torch.testing.assert_close(ss_out.cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
@@ -157,7 +163,7 @@ def test_gemv_epilogues(dev, M, rows):
     x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
     W = _weights(dev, N, Kd, 22, rows=2 * N)
     y = torch.empty(M, N, device=dev, dtype=BF)
-    gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)(x, W, y=y, nw=nw, cfg=(rows,))
+    gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)(x, W, y=y, nw=nw, cfg=rows)
     torch.cuda.synchronize()
     want = O.gemv(x.cpu(), W.cpu(), O.EPI_SWIGLU, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
     assert_bf16_close(y.cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
@@ -166,14 +172,14 @@ def test_gemv_epilogues(dev, M, rows):
     a = torch.randn(M, Kd, device=dev, generator=g).to(BF)
     W = _weights(dev, N, Kd, 23)
     y = torch.empty(M, N, device=dev, dtype=BF)
-    gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)(a, W, y=y, cfg=(rows,))
+    gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)(a, W, y=y, cfg=rows)
     torch.cuda.synchronize()
     want = O.gemv(a.cpu(), W.cpu(), O.EPI_BF16)
     assert_bf16_close(y.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
 
 
-@pytest.mark.parametrize("M", [1, 16])
-def test_lm_head_argmax_and_graph_replay(dev, M):
+@pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (16, (0, 8, 0))])
+def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     _, gemv = K()
     V, H = 151936, 2560
     g = _g(dev, 30)
@@ -181,10 +187,13 @@ def test_lm_head_argmax_and_graph_replay(dev, M):
     x = torch.randn(M, H, device=dev, generator=g).to(BF)
     nw = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(BF)
     op = gemv.Gemv(M, V, H, gemv.EPI_ARGMAX, norm=True)
+    op.cfg = cfg
     logits = torch.empty(M, V, device=dev, dtype=BF)
     ids = torch.empty(M, device=dev, dtype=torch.int64)
-    op(x, E, y=logits, nw=nw, ids=ids)
+    pos = torch.arange(M, device=dev, dtype=torch.int32)
+    op(x, E, y=logits, nw=nw, ids=ids, pos_inc=pos)
     torch.cuda.synchronize()
+    assert torch.equal(pos.cpu(), torch.arange(M, dtype=torch.int32) + 1)
     # self-consistent: ids is the first maximum of the kernel's own bf16 logits
     assert torch.equal(ids.cpu(), O.argmax_first(logits.cpu()))
     # close to the oracle, and the chosen logit is the oracle's maximum within 1 ulp
