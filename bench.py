@@ -43,6 +43,20 @@ def parse_args():
     return ap.parse_args()
 
 
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "attn_kernel_b16_ctx8192_pmc.json")
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the partial kernel from the committed FETCH_SIZE /
+    WRITE_SIZE summary (two rocprofv3 --pmc passes, calibrated on a 1 GiB copy)."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def attn_bytes():
     return 2 * B * NKV * CTX * D * 2 + 2 * B * NQ * D * 2
 
@@ -230,7 +244,7 @@ def bench_attention(args):
         "wall_s_timed": round(wall, 4),
         "roofline": {"bound": "hbm", "kernel": "attn_kernel<1, false, false> (split-K partials)",
                      "achieved": round(k_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
                      "avg_kernel_us": round(k_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": nbytes},
         "measured_copy_gbs": round(copy_gbs, 1),

@@ -130,15 +130,17 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *              (torch.argmax at engine/engine.py:291, fused into the LM head);
  *              bf16 logits stored in y when y != NULL; pos_inc[m] += 1 when
  *              pos_inc != NULL (the step's position advance, engine.py:292);
+ *              next_h[m] = next_emb[ids[m]] ([N, K] table) when both are given
+ *              (the next step's embedding gather, gemv.py:201-211);
  *              part: fp32 scratch of part_len >= ko_gemv_argmax_scratch(...).
  * layout 0: each 256-thread workgroup owns `rows` (4 or 8) columns; any M.
  * layout 1: each wavefront owns `rows` (1, 2, 4) columns, `waves` (2, 4)
  *           wavefronts per workgroup; M <= 4 per launch slice.
  * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
-            float* ss_out, long long* ids, int* pos_inc, float* part, long long part_len, int M,
-            int N, int K, int epi, int norm, int accumulate, int layout, int rows, int waves,
-            float eps, void* stream);
+            float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
+            float* part, long long part_len, int M, int N, int K, int epi, int norm,
+            int accumulate, int layout, int rows, int waves, float eps, void* stream);
 
 /* Number of fp32 scratch elements epi 4 (ARGMAX) needs for N columns with this
  * launch configuration (a size, not a status; -1 for bad arguments). Helper of

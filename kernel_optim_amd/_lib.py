@@ -40,8 +40,8 @@ SIGNATURES = {
     "ko_silu_mul": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
     "ko_embed_ss": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _c_void_p],
     "ko_gemv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                _c_void_p, _c_void_p, _c_void_p, _ll, _int, _int, _int, _int, _int, _int, _int,
-                _int, _int, _f, _c_void_p],
+                _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _ll, _int, _int, _int, _int,
+                _int, _int, _int, _int, _int, _f, _c_void_p],
     "ko_gemv_argmax_scratch": [_int, _int, _int, _int],
 }
 

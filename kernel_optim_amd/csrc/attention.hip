@@ -166,42 +166,46 @@ __device__ __forceinline__ void norm_rope_head(const uint4 (&x)[4], const uint4 
   }
 }
 
-// Log-sum-exp merge of n unit partials of row R (one wavefront; lane owns
-// head-dim elements 2l, 2l+1), normalise, round to bf16. Latency-lean: lane c
-// loads (m_c, l_c) for all units at once and computes the unit weight
-// w_c = 2^(m_c - M); the partial accumulators are then loaded 16 units at a
-// time with no dependence between the loads of a batch.
+// Log-sum-exp merge of the unit partials of row R (one wavefront; lane owns
+// head-dim elements 2l, 2l+1), normalise, round to bf16. The row's unit count
+// is n = nunits(kv_len); the loads of (m, l) and of the accumulators are issued
+// for all max_units slots (32 per batch, every slot in bounds) together with
+// the length, so a merge costs one memory round trip; slots >= n are masked.
+// Pass n >= 0 when it is known already (then len_ptr is unused).
 __device__ void combine_row(const float* __restrict__ o_part, const float* __restrict__ ml,
-                            long long R, int n, int max_units, uint16_t* __restrict__ out) {
+                            long long R, int n, const int* len_ptr, int len_off, int cap,
+                            int unit, int max_units, uint16_t* __restrict__ out) {
   const int lane = lane_id();
   const float2* mlr = reinterpret_cast<const float2*>(ml) + R * max_units;
   const float* op = o_part + R * max_units * D + 2 * lane;
-  float L = 0.f, o0 = 0.f, o1 = 0.f;
-  float M = NEG_BIG;
-  for (int c = lane; c < n; c += 64) M = fmaxf(M, mlr[c].x);
-  M = wave_max(M);
-  for (int c0 = 0; c0 < n; c0 += 64) {
-    const int c = c0 + lane;
-    float wl = 0.f, w = 0.f;
-    if (c < n) {
-      const float2 mlc = mlr[c];
-      w = __builtin_amdgcn_exp2f(mlc.x - M);
-      wl = w * mlc.y;
+  float L = 0.f, o0 = 0.f, o1 = 0.f, M = NEG_BIG;
+  for (int c0 = 0; c0 < max_units; c0 += 32) {
+    const int cn = min(32, max_units - c0);
+    const float2 mlc = lane < cn ? mlr[c0 + lane] : make_float2(NEG_BIG, 0.f);
+    float2 a[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      if (j < cn) a[j] = *reinterpret_cast<const float2*>(op + (long long)(c0 + j) * D);
+    if (n < 0) {
+      int l = *len_ptr + len_off;
+      n = nunits(l < cap ? l : cap, unit);
     }
-    L += wave_sum(wl);
-    const int cn = min(64, n - c0);
-    for (int j0 = 0; j0 < cn; j0 += 16) {
-      float2 a16[16];
+    const int valid = min(cn, max(0, n - c0));
+    if (valid <= 0) break;
+    const float mc = lane < valid ? mlc.x : NEG_BIG;
+    const float Mn = fmaxf(M, wave_max(mc));
+    const float scale_old = __builtin_amdgcn_exp2f(M - Mn);
+    const float w = lane < valid ? __builtin_amdgcn_exp2f(mc - Mn) : 0.f;
+    L = L * scale_old + wave_sum(lane < valid ? w * mlc.y : 0.f);  // stale slots may hold NaN
+    o0 *= scale_old;
+    o1 *= scale_old;
+    M = Mn;
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (j0 + j < cn) a16[j] = *reinterpret_cast<const float2*>(op + (long long)(c0 + j0 + j) * D);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (j0 + j < cn) {
-          const float wj = __shfl(w, j0 + j, 64);
-          o0 += wj * a16[j].x;
-          o1 += wj * a16[j].y;
-        }
+    for (int j = 0; j < 32; ++j) {
+      if (j < valid) {
+        const float wj = __shfl(w, j, 64);
+        o0 += wj * a[j].x;
+        o1 += wj * a[j].y;
       }
     }
   }
@@ -215,24 +219,43 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   static_assert(!QKV || T == 1, "the QKV prologue serves one decode token per sequence");
   __shared__ __align__(16) uint16_t lds_p[WAVES][T][G][16];
 
+  const int wpb = blockDim.x >> 6;   // wavefronts per workgroup (1..WAVES)
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;   // key slot of the QK lanes / column chunk of the PV lanes
   const int g = lane >> 4;   // MFMA k-group / PV key row
   const int nkv = a.nkv, nq = nkv * G, unit = a.unit, max_units = a.max_units;
-  const int W = gridDim.x * WAVES;
-  const int total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
+  const int W = gridDim.x * wpb;
   uint16_t* myp = &lds_p[wave][0][0][0];
 
-  for (int u = blockIdx.x * WAVES + wave; u < total; u += W) {
+  // Up to 64 sequences: one load of the lengths and one prefix scan serve
+  // every unit this wave processes (lane b holds sequence b's unit count and
+  // inclusive prefix).
+  const bool small_b = a.B <= 64;
+  int my_n = 0, my_incl = 0, total;
+  if (small_b) {
+    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap), unit) : 0;
+    my_incl = wave_incl_scan(my_n);
+    total = readlane(my_incl, 63) * nkv;
+  } else {
+    total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
+  }
+
+  for (int u = blockIdx.x * wpb + wave; u < total; u += W) {
     const int pidx = u / nkv;
     const int kvh = u - pidx * nkv;
-    int b, c;
-    locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
-    b = uniform(b);
-    c = uniform(c);
-    if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
-    const int kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+    int b, c, kv_len;
+    if (small_b) {
+      b = uniform(__popcll(__ballot(my_incl <= pidx)));
+      c = pidx - readlane(my_incl - my_n, b);
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+    } else {
+      locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
+      b = uniform(b);
+      c = uniform(c);
+      if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+    }
     const int k0 = c * unit;
     const int k1 = min(k0 + unit, kv_len);
     const uint16_t* kb = a.kc + (long long)b * a.cb + (long long)kvh * a.ch;
@@ -501,8 +524,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (int t = 0; t < T; ++t)
 #pragma unroll
           for (int j = 0; j < G; ++j)
-            combine_row(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, max_units,
-                        a.out);
+            combine_row(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, nullptr, 0,
+                        a.cap, unit, max_units, a.out);
         if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -514,11 +537,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
     const float* __restrict__ o_part, const float* __restrict__ ml,
     const int* __restrict__ lens, int len_off, int cap, int T, int nq, int rows, int unit,
     int max_units, uint16_t* __restrict__ out) {
-  const int R = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int R = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (R >= rows) return;
   const int b = R / (T * nq);
-  const int n = nunits(seq_len(lens, b, len_off, cap), unit);
-  combine_row(o_part, ml, R, n, max_units, out);
+  combine_row(o_part, ml, R, -1, lens + b, len_off, cap, unit, max_units, out);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -539,7 +561,9 @@ int check_common(const void* kc, const void* vc, const int* lens, int cap, long 
 
 template <int T, bool QKV, bool FUSED>
 int launch(const AttnArgs& a, int grid_waves, hipStream_t s) {
-  const dim3 grid((grid_waves + WAVES - 1) / WAVES), block(64 * WAVES);
+  // Small grids run one wavefront per workgroup so they spread over more CUs.
+  const int wpb = grid_waves <= 1024 ? 1 : WAVES;
+  const dim3 grid((grid_waves + wpb - 1) / wpb), block(64 * wpb);
   hipLaunchKernelGGL((attn_kernel<T, QKV, FUSED>), grid, block, 0, s, a);
   return KO_LAUNCH_STATUS();
 }
@@ -603,7 +627,8 @@ int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_l
   if (B < 1 || T < 1 || nq < 1 || unit < 1 || (long long)max_units * unit < cap) return KO_EINVAL;
   if (!aligned16(out)) return KO_EINVAL;
   const int rows = B * T * nq;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((rows + WAVES - 1) / WAVES), dim3(64 * WAVES), 0,
+  const int wpb = rows <= 1024 ? 1 : WAVES;  // small merges: spread rows over more CUs
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((rows + wpb - 1) / wpb), dim3(64 * wpb), 0,
                      static_cast<hipStream_t>(stream), o_part, ml, kv_lens, len_offset, cap, T,
                      nq, rows, unit, max_units, static_cast<uint16_t*>(out));
   return KO_LAUNCH_STATUS();

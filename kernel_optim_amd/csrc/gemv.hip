@@ -418,44 +418,62 @@ __global__ __launch_bounds__(64 * WPB) void gemv_wave_kernel(GemvArgs a) {
   }
 }
 
-// One workgroup per row m: argmax over the work units' (value, index) pairs,
-// lowest index on ties; optionally pos[m] += 1 (the decode step's position
-// advance, engine.py:292).
-__global__ __launch_bounds__(NT) void argmax_finalize_kernel(const float2* __restrict__ part,
-                                                             int nparts, long long* __restrict__ ids,
-                                                             int* __restrict__ pos) {
-  __shared__ float2 s_best[NT / 64];
+// One 1024-thread workgroup per row m: argmax over the work units' (value,
+// index) pairs with the lowest index on ties, loads issued 8 per thread at a
+// time. Optionally pos[m] += 1 (the decode step's position advance,
+// engine.py:292) and h[m] = emb[ids[m]] (the next step's embedding gather,
+// gemv.py:201-211, so the next step needs no gather launch).
+constexpr int FT = 1024;
+__device__ __forceinline__ void better(float v, int i, float& bv, int& bi) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+__global__ __launch_bounds__(FT) void argmax_finalize_kernel(
+    const float2* __restrict__ part, int nparts, long long* __restrict__ ids,
+    int* __restrict__ pos, const uint16_t* __restrict__ emb, uint16_t* __restrict__ h, int H,
+    int V) {
+  __shared__ float2 s_best[FT / 64];
+  __shared__ int s_id;
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const float2* pr = part + (long long)m * nparts;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = t; i < nparts; i += NT) {
-    const float2 c = part[(long long)m * nparts + i];
-    const int ci = __float_as_int(c.y);
-    if (c.x > bv || (c.x == bv && ci < bi)) {
-      bv = c.x;
-      bi = ci;
+  for (int i0 = t; i0 < nparts; i0 += 8 * FT) {
+    float2 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + j * FT;
+      c[j] = i < nparts ? pr[i] : make_float2(-INFINITY, __int_as_float(0x7fffffff));
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) better(c[j].x, __float_as_int(c[j].y), bv, bi);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
+    better(ov, oi, bv, bi);
   }
   if (lane == 0) s_best[wv] = make_float2(bv, __int_as_float(bi));
   __syncthreads();
   if (t == 0) {
-    float2 best = s_best[0];
-    for (int i = 1; i < NT / 64; ++i) {
-      const float2 c = s_best[i];
-      if (c.x > best.x || (c.x == best.x && __float_as_int(c.y) < __float_as_int(best.y)))
-        best = c;
-    }
-    ids[m] = __float_as_int(best.y);
+    float2 b = s_best[0];
+    float v = b.x;
+    int i = __float_as_int(b.y);
+    for (int w = 1; w < FT / 64; ++w) better(s_best[w].x, __float_as_int(s_best[w].y), v, i);
+    ids[m] = i;
     if (pos) pos[m] += 1;
+    s_id = i;
+  }
+  if (emb) {
+    __syncthreads();
+    const long long tok = s_id;
+    if (tok >= 0 && tok < V) {
+      for (int c = t; c < (H >> 3); c += FT)
+        *reinterpret_cast<uint4*>(h + (long long)m * H + 8 * c) = ldg16(emb + tok * H + 8 * c);
+    }
   }
 }
 
@@ -531,9 +549,9 @@ long long parts_for(int N, int layout, int rows, int waves) {
 extern "C" {
 
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
-            float* ss_out, long long* ids, int* pos_inc, float* part, long long part_len, int M,
-            int N, int K, int epi, int norm, int accumulate, int layout, int rows, int waves,
-            float eps, void* stream) {
+            float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
+            float* part, long long part_len, int M, int N, int K, int epi, int norm,
+            int accumulate, int layout, int rows, int waves, float eps, void* stream) {
   if (!x || !w || M < 1 || N < 1 || K < 8 || (K & 7)) return KO_EINVAL;
   if (epi < EPI_F32 || epi > EPI_ARGMAX) return KO_EINVAL;
   if (!al16(x) || !al16(w)) return KO_EINVAL;
@@ -553,6 +571,8 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
   if (epi == EPI_ARGMAX) {
     if (!ids || !part) return KO_EINVAL;
     if (part_len < 2LL * mstep * nparts) return KO_ERANGE;
+    if ((next_emb == nullptr) != (next_h == nullptr)) return KO_EINVAL;
+    if (next_emb && (!al16(next_emb) || !al16(next_h))) return KO_EINVAL;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   for (int m0 = 0; m0 < M; m0 += mstep) {
@@ -583,8 +603,11 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
       st = launch_wave_cfg(a, epi, norm != 0, rows, waves, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
-      hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(NT), 0, s, a.part, a.nparts,
-                         ids + m0, pos_inc ? pos_inc + m0 : nullptr);
+      hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(FT), 0, s, a.part, a.nparts,
+                         ids + m0, pos_inc ? pos_inc + m0 : nullptr,
+                         static_cast<const uint16_t*>(next_emb),
+                         next_h ? static_cast<uint16_t*>(next_h) + (long long)m0 * K : nullptr, K,
+                         N);
       st = KO_LAUNCH_STATUS();
       if (st) return st;
     }

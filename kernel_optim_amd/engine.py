@@ -20,8 +20,9 @@ attention launch):
   qkv GEMV (RMSNorm prologue) -> attention (q/k norm + RoPE + KV append
   prologue, split-K partials, last-unit LSE combine) -> o GEMV (+residual) ->
   gate/up GEMV (RMSNorm prologue, SwiGLU epilogue) -> down GEMV (+residual)
-and around the layers the embedding gather and the LM head with the greedy
-argmax fused into it (its finalize kernel also advances the positions). Replays are pipelined: the next step is queued before
+and after the layers the LM head with the greedy argmax fused into it; its
+finalize kernel also advances the positions and gathers the chosen tokens'
+embedding rows, the next step's input. Replays are pipelined: the next step is queued before
 the host waits for the previous step's ids (engine.py:509-522).
 """
 
@@ -147,8 +148,7 @@ class Engine:
         """One decode token per sequence at pos[b]; greedy ids; positions advance."""
         cfg = self.cfg
         g = {k: v[0] for k, v in self.gv.items()}
-        h = self.h
-        embed_ss(self.ids, self.w["embed"], h, None)
+        h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
         for i, lw in enumerate(self.w["layers"]):
             g["qkv"](h, lw["qkv"], y=self.qkv, nw=lw["w_in"])
             self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
@@ -158,7 +158,7 @@ class Engine:
             g["gu"](h, lw["gu"], y=self.act, nw=lw["w_post"])
             g["down"](self.act, lw["down"], h=h)
         g["lm"](h, self.w["lm_head"], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
-                pos_inc=self.pos)
+                pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
 
     def _capture(self, fn):
         # Warm up on a side stream, then capture. Warm-up steps write cache slot 0,
@@ -184,6 +184,7 @@ class Engine:
                               self._sin)
         self.ids.copy_(ids)
         self.pos.fill_(prompt.shape[1])
+        embed_ss(self.ids, self.w["embed"], self.h, None)   # the first decode step's input
         if self.logits is not None:
             self.logits.copy_(logits)
 

@@ -67,7 +67,10 @@ class Gemv:
         return self._part
 
     def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None,
-                 pos_inc=None):
+                 pos_inc=None, next_emb=None, next_h=None):
+        """ARGMAX extras: ``pos_inc`` ([M] int32) is advanced by one; with
+        ``next_emb`` ([N, K] bf16, the embedding) the chosen ids' rows are gathered
+        into ``next_h`` ([M, K] bf16), the next decode step's input."""
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
@@ -90,10 +93,15 @@ class Gemv:
                 _check(y, "y", BF16, (M, N))
             if pos_inc is not None:
                 _check(pos_inc, "pos_inc", torch.int32, (M,))
+            _need((next_emb is None) == (next_h is None), "next_emb and next_h go together")
+            if next_emb is not None:
+                _check(next_emb, "next_emb", BF16, (N, K))
+                _check(next_h, "next_h", BF16, (M, K))
         part = self._scratch(x.device, (layout, rows, waves)) if epi == EPI_ARGMAX else None
         _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
                   _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
-                  _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(pos_inc), _lib.ptr(part),
+                  _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(pos_inc),
+                  _lib.ptr(next_emb), _lib.ptr(next_h), _lib.ptr(part),
                   0 if part is None else part.numel(), M, N, K, epi, int(self.norm), 0, layout,
                   rows, waves, self.eps, _lib.stream_ptr())
 

@@ -191,9 +191,11 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     logits = torch.empty(M, V, device=dev, dtype=BF)
     ids = torch.empty(M, device=dev, dtype=torch.int64)
     pos = torch.arange(M, device=dev, dtype=torch.int32)
-    op(x, E, y=logits, nw=nw, ids=ids, pos_inc=pos)
+    nxt = torch.zeros(M, H, device=dev, dtype=BF)
+    op(x, E, y=logits, nw=nw, ids=ids, pos_inc=pos, next_emb=E, next_h=nxt)
     torch.cuda.synchronize()
     assert torch.equal(pos.cpu(), torch.arange(M, dtype=torch.int32) + 1)
+    assert torch.equal(nxt, E[ids])
     # self-consistent: ids is the first maximum of the kernel's own bf16 logits
     assert torch.equal(ids.cpu(), O.argmax_first(logits.cpu()))
     # close to the oracle, and the chosen logit is the oracle's maximum within 1 ulp
