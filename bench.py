@@ -40,6 +40,10 @@ def parse_args():
                     help="skip the attention measurement (profiling the decode step alone)")
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--new-tokens", type=int, default=256)
+    ap.add_argument("--decode-b16", action="store_true",
+                    help="also measure B=16 decode (same workload at batch 16)")
+    ap.add_argument("--layer", action="store_true",
+                    help="also measure one fused decoder layer at B=1, 4, 16 with 2048 cached keys")
     return ap.parse_args()
 
 
@@ -92,17 +96,18 @@ def cpu_baseline(seconds):
     }
 
 
-def bench_decode(args):
+def bench_decode(args, eng=None, B=1):
     """Qwen3-4B architecture (36 layers, random N(0,0.02) bf16 weights, seed 0),
-    B=1, prompt of seeded uniform-random ids, greedy decode of ``new_tokens``
+    batch B, prompts of seeded uniform-random ids, greedy decode of ``new_tokens``
     through Engine.generate (hipGraph step, pipelined replays). tok/s counts the
-    decode steps after the first token (which comes from the prefill)."""
+    decode steps after the first token (which comes from the prefill), over all
+    B sequences."""
     import torch
     from kernel_optim_amd.engine import Engine
-    eng = Engine("random")
+    eng = eng or Engine("random")
     cfg = eng.cfg
     S, N = args.prompt, args.new_tokens
-    prompt = torch.randint(0, cfg.vocab, (1, S), generator=torch.Generator().manual_seed(0)).tolist()
+    prompt = torch.randint(0, cfg.vocab, (B, S), generator=torch.Generator().manual_seed(0)).tolist()
     for _ in eng.generate(prompt, N):      # setup, tuning, capture, warm-up
         pass
     torch.cuda.synchronize()
@@ -113,14 +118,14 @@ def bench_decode(args):
             t0 = time.perf_counter()
         out.append(toks[0])
     el = time.perf_counter() - t0
-    tok_s = (N - 1) / el
+    tok_s = B * (N - 1) / el
     step_ms = eng.time_step(min(50, N - 1))
     kv_per_key = cfg.layers * 2 * cfg.nkv * cfg.head_dim * 2
     avg_keys = S + 1 + (N - 2) / 2.0            # keys read by decode steps 1..N-1
-    step_bytes = cfg.weight_bytes_per_step() + kv_per_key * avg_keys + kv_per_key
-    roof_tok_s = PEAK_HBM_GBS * 1e9 / step_bytes
+    step_bytes = cfg.weight_bytes_per_step() + B * (kv_per_key * avg_keys + kv_per_key)
+    roof_tok_s = B * PEAK_HBM_GBS * 1e9 / step_bytes
     res = {
-        "workload": f"Qwen3-4B architecture greedy decode, B=1, prompt {S}, {N} new tokens, "
+        "workload": f"Qwen3-4B architecture greedy decode, B={B}, prompt {S}, {N} new tokens, "
                     "random-init bf16 weights (seed 0), hipGraph decode step",
         "tok_s": round(tok_s, 2),
         "ms_per_token": round(1e3 / tok_s, 4),
@@ -128,12 +133,91 @@ def bench_decode(args):
         "bytes_per_step": int(step_bytes),
         "roofline": {"bound": "hbm", "tok_s_at_peak": round(roof_tok_s, 1),
                      "frac": round(tok_s / roof_tok_s, 4),
-                     "achieved_gbs": round(step_bytes / (1e3 / tok_s) / 1e6, 1),
+                     "achieved_gbs": round(step_bytes * tok_s / B / 1e9, 1),
                      "graph_step_frac": round((step_bytes / (step_ms * 1e-3) / 1e9) / PEAK_HBM_GBS, 4)},
         "first_tokens": out[:8],
     }
-    if not args.no_cpu:
+    if not args.no_cpu and B == 1:
         res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
+    return res
+
+
+def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
+    """One fused Qwen3-4B decoder layer decode step (qkv GEMV with RMSNorm prologue,
+    attention with q/k norm + RoPE + KV append at position 2048, combine, o GEMV +
+    residual, gate/up GEMV with RMSNorm + SwiGLU, down GEMV + residual), random
+    N(0, 0.02) weights, 2048 cached keys. ``nsets`` independent layers (weights and
+    caches) are rotated so the Infinity Cache cannot serve a replay; the replays
+    are captured in one graph and timed with events."""
+    import torch
+    from kernel_optim_amd.kernels.fused import DecodeAttention
+    from kernel_optim_amd.kernels.gemv import EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv
+    from kernel_optim_amd.engine import _rope_tables
+    from kernel_optim_amd.model import Qwen3Config, random_weights
+    cfg = Qwen3Config(layers=nsets)
+    dev = torch.device("cuda:0")
+    w = random_weights(cfg, seed=1, device=dev)
+    cap = ctx + 16
+    cos, sin = _rope_tables(cap, cfg.head_dim, cfg.theta, dev)
+    res = {}
+    for B in Bs:
+        g = torch.Generator(device=dev).manual_seed(B)
+        kc = [torch.randn(B, cfg.nkv, cap, cfg.head_dim, device=dev, generator=g).to(torch.bfloat16)
+              for _ in range(nsets)]
+        vc = [torch.randn_like(k) for k in kc]
+        pos = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        h = torch.randn(B, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+        qkv = torch.empty(B, cfg.nqkv, device=dev, dtype=torch.bfloat16)
+        att_out = torch.empty(B, cfg.nq * cfg.head_dim, device=dev, dtype=torch.bfloat16)
+        act = torch.empty(B, cfg.inter, device=dev, dtype=torch.bfloat16)
+        att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
+        H = cfg.hidden
+        L = w["layers"]
+        e = cfg.eps
+        ops = dict(qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
+                   o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
+                   gu=Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
+                   down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e))
+        for name, key in (("qkv", "qkv"), ("o", "o"), ("gu", "gu"), ("down", "down")):
+            ops[name].tune([l[key] for l in L], time.monotonic() + 20)
+
+        def layer(i):
+            lw = L[i]
+            ops["qkv"](h, lw["qkv"], y=qkv, nw=lw["w_in"])
+            att.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i], att_out,
+                           cfg.eps)
+            ops["o"](att_out, lw["o"], h=h)
+            ops["gu"](h, lw["gu"], y=act, nw=lw["w_post"])
+            ops["down"](act, lw["down"], h=h)
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(nsets):
+                layer(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(nsets):
+                layer(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * nsets)
+        nbytes = cfg.layer_bytes() + B * (ctx + 1) * cfg.nkv * cfg.head_dim * 2 * 2 + \
+            B * cfg.nkv * cfg.head_dim * 2 * 2
+        res[f"B{B}"] = {"us_per_layer": round(us, 2), "bytes": int(nbytes),
+                        "gbs": round(nbytes / us / 1e3, 1),
+                        "roofline_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                        "gemv_cfgs": {k: v.cfg for k, v in ops.items()}}
+        del kc, vc
+        torch.cuda.empty_cache()
     return res
 
 
@@ -242,7 +326,8 @@ def bench_attention(args):
                    "unit_keys": att.unit, "grid_waves": att.grid_waves},
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "wall_s_timed": round(wall, 4),
-        "roofline": {"bound": "hbm", "kernel": "attn_kernel<1, false, false> (split-K partials)",
+        "roofline": {"bound": "hbm",
+                     "kernel": f"attn1_kernel<false, {att.waves_per_unit}> (split-K partials)",
                      "achieved": round(k_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
                      "avg_kernel_us": round(k_ms * 1e3, 3),
@@ -267,7 +352,15 @@ def main():
         if not args.no_cpu:
             line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     if not args.no_decode:
-        line["decode_b1"] = bench_decode(args)
+        from kernel_optim_amd.engine import Engine
+        eng = Engine("random")
+        line["decode_b1"] = bench_decode(args, eng, B=1)
+        if args.decode_b16:
+            line["decode_b16"] = bench_decode(args, eng, B=16)
+        del eng
+        torch.cuda.empty_cache()
+    if args.layer:
+        line["layer_2048"] = bench_layer()
     print(json.dumps(line), flush=True)
 
 

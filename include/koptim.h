@@ -28,8 +28,12 @@ extern "C" {
  * kv_lens  [B] int32 on the device; valid keys of sequence b are
  *          kv_lens[b] + len_offset (the reference passes pos with T: offset T).
  *          Query t sits at position valid-T+t and sees keys < valid-T+t+1.
- * unit     keys per work unit (multiple of 16); max_units*unit >= cap.
- * grid_waves  number of wavefronts launched (they stride over the units).
+ * unit     keys per work unit (multiple of 16); max_units*unit >= cap. Each unit
+ *          leaves one fp32 partial slot per query row.
+ * grid_waves  number of wavefronts launched (they stride over the units). With
+ *          T == 1 (and no counters) a unit is split over the wavefronts of one
+ *          workgroup: 4 when unit % 64 == 0, else 2 when unit % 32 == 0, else 1,
+ *          so grid_waves should be a multiple of that count.
  * o_part   [B*T*nq*max_units*head_dim] fp32 scratch, ml [B*T*nq*max_units*2] fp32.
  * T in 1..4, head_dim 128. */
 int ko_decode_attn_partial(const void* q, const void* k_cache, const void* v_cache,

@@ -136,8 +136,7 @@ __device__ __forceinline__ void norm_rope_head(const uint4 (&x)[4], const uint4 
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += xf[i][e] * xf[i][e];
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
+  ss = sum_xor32(sum_xor16(ss));
   const float rstd = rsqrtf(ss / (float)D + eps);
   float xn[4][8];
 #pragma unroll
@@ -169,9 +168,10 @@ __device__ __forceinline__ void norm_rope_head(const uint4 (&x)[4], const uint4 
 // Log-sum-exp merge of the unit partials of row R (one wavefront; lane owns
 // head-dim elements 2l, 2l+1), normalise, round to bf16. The row's unit count
 // is n = nunits(kv_len); the loads of (m, l) and of the accumulators are issued
-// for all max_units slots (32 per batch, every slot in bounds) together with
-// the length, so a merge costs one memory round trip; slots >= n are masked.
-// Pass n >= 0 when it is known already (then len_ptr is unused).
+// for up to NB slots at a time (every slot in bounds) together with the length,
+// so a merge of up to NB slots costs one memory round trip; slots >= n are
+// masked. Pass n >= 0 when it is known already (then len_ptr is unused).
+template <int NB>
 __device__ void combine_row(const float* __restrict__ o_part, const float* __restrict__ ml,
                             long long R, int n, const int* len_ptr, int len_off, int cap,
                             int unit, int max_units, uint16_t* __restrict__ out) {
@@ -179,12 +179,13 @@ __device__ void combine_row(const float* __restrict__ o_part, const float* __res
   const float2* mlr = reinterpret_cast<const float2*>(ml) + R * max_units;
   const float* op = o_part + R * max_units * D + 2 * lane;
   float L = 0.f, o0 = 0.f, o1 = 0.f, M = NEG_BIG;
-  for (int c0 = 0; c0 < max_units; c0 += 32) {
-    const int cn = min(32, max_units - c0);
+  static_assert(NB <= 64, "one (m, l) slot per lane");
+  for (int c0 = 0; c0 < max_units; c0 += NB) {
+    const int cn = min(NB, max_units - c0);
     const float2 mlc = lane < cn ? mlr[c0 + lane] : make_float2(NEG_BIG, 0.f);
-    float2 a[32];
+    float2 a[NB];
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
+    for (int j = 0; j < NB; ++j)
       if (j < cn) a[j] = *reinterpret_cast<const float2*>(op + (long long)(c0 + j) * D);
     if (n < 0) {
       int l = *len_ptr + len_off;
@@ -201,9 +202,9 @@ __device__ void combine_row(const float* __restrict__ o_part, const float* __res
     o1 *= scale_old;
     M = Mn;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
+    for (int j = 0; j < NB; ++j) {
       if (j < valid) {
-        const float wj = __shfl(w, j, 64);
+        const float wj = readlane(w, j);
         o0 += wj * a[j].x;
         o1 += wj * a[j].y;
       }
@@ -477,10 +478,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       for (int j = 0; j < G; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float v = acc[t][j][e];
-          v += __shfl_xor(v, 16, 64);
-          v += __shfl_xor(v, 32, 64);
-          acc[t][j][e] = v;
+          acc[t][j][e] = sum_xor32(sum_xor16(acc[t][j][e]));
         }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -524,11 +522,323 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (int t = 0; t < T; ++t)
 #pragma unroll
           for (int j = 0; j < G; ++j)
-            combine_row(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, nullptr, 0,
+            combine_row<32>(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, nullptr, 0,
                         a.cap, unit, max_units, a.out);
         if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+  }
+}
+
+// RMSNorm + RoPE of one head held two elements per lane (lane l: elements 2l,
+// 2l+1), the cast chain of fused.py:71-87: xn = bf16(w * bf16(x * rstd)),
+// y = bf16(bf16(xn * cos) + bf16(rotate_half(xn) * sin)). rotate_half's partner
+// of element d (d +- 64) sits 32 lanes away. Returns y packed as 2 bf16. Call
+// with all 64 lanes active.
+__device__ __forceinline__ uint32_t norm_rope2(uint32_t x, uint32_t w, uint32_t cw, uint32_t sw,
+                                               float eps) {
+  const float x0 = bf16lo(x), x1 = bf16hi(x);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rstd = rsqrtf(ss / (float)D + eps);
+  const float n0 = round_bf16(bf16lo(w) * round_bf16(x0 * rstd));
+  const float n1 = round_bf16(bf16hi(w) * round_bf16(x1 * rstd));
+  const uint32_t nb = pack_bf16x2(n0, n1);  // exact: n0, n1 are bf16 values
+  const auto sw32 = __builtin_amdgcn_permlane32_swap(nb, nb, false, false);
+  const bool lo_half = lane_id() < 32;
+  const uint32_t pb = lo_half ? (uint32_t)sw32[1] : (uint32_t)sw32[0];
+  const float r0 = lo_half ? -bf16lo(pb) : bf16lo(pb);
+  const float r1 = lo_half ? -bf16hi(pb) : bf16hi(pb);
+  const float y0 = round_bf16(n0 * bf16lo(cw)) + round_bf16(r0 * bf16lo(sw));
+  const float y1 = round_bf16(n1 * bf16hi(cw)) + round_bf16(r1 * bf16hi(sw));
+  return pack_bf16x2(y0, y1);
+}
+
+// One decode token per sequence (T = 1) with WM wavefronts per workgroup. A
+// unit of `unit` keys of one (b, kv_head) pair is split into WM contiguous
+// sub-ranges of sub = unit / WM keys, one per wavefront; the wavefronts'
+// partials are merged through LDS, so a unit stores a single fp32 (m, l, acc)
+// slot and the combine reads few slots. Per unit:
+//   - every global load is issued before any wait (K/V of the first 16-key
+//     step, the q inputs, the new k/v inputs), so they cost one round trip;
+//   - QKV: the workgroup norms and ropes its 4 q heads once, G / WM heads per
+//     wavefront at two elements per lane, and wavefront 0 of the unit that
+//     holds the new key position also the new k (and appends k and v to the
+//     cache); the heads go through LDS into the MFMA operand layout;
+//   - the 16-key step is the T = 1 case of attn_kernel's: every 16-lane row of
+//     the QK^T result holds the same 16 scores (the A rows are the 4 heads
+//     replicated), so the running max stays wave-uniform without cross-row
+//     traffic.
+template <bool QKV, int WM>
+__global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
+  __shared__ __align__(16) uint16_t lds_p[WM][G * 16];
+  __shared__ __align__(16) float lds_acc[WM][4][G][D];  // [wave][key group g][head][col]
+  __shared__ float lds_ml[WM][G][2];
+  __shared__ __align__(16) uint32_t lds_q[G][D / 2];     // QKV: roped q heads (bf16 pairs)
+  __shared__ __align__(16) uint32_t lds_k[D / 2];        // QKV: roped new key
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int nkv = a.nkv, nq = nkv * G, unit = a.unit, max_units = a.max_units;
+  const int sub = unit / WM;
+  uint16_t* myp = lds_p[wave];
+
+  const bool small_b = a.B <= 64;
+  int my_n = 0, my_incl = 0, total;
+  if (small_b) {
+    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap), unit) : 0;
+    my_incl = wave_incl_scan(my_n);
+    total = readlane(my_incl, 63) * nkv;
+  } else {
+    total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
+  }
+
+  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const int pidx = u / nkv;
+    const int kvh = u - pidx * nkv;
+    int b, c, kv_len;
+    if (small_b) {
+      b = uniform(__popcll(__ballot(my_incl <= pidx)));
+      c = pidx - readlane(my_incl - my_n, b);
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+    } else {
+      locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
+      b = uniform(b);
+      c = uniform(c);
+      if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+    }
+    const int ku1 = min((c + 1) * unit, kv_len);
+    const int k0 = c * unit + wave * sub;
+    const int k1 = min(k0 + sub, ku1);
+    const bool active = k0 < k1;  // the last unit of a sequence may leave waves idle
+    const int pnew = kv_len - 1;
+    const bool new_unit = QKV && pnew < ku1;  // this unit holds the new key position
+    const bool has_new = new_unit && active && k0 <= pnew && pnew < k1;
+
+    float mu[G], lsum[G], acc[G][8];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      mu[j] = NEG_BIG;
+      lsum[j] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+    }
+
+    const uint16_t* kb = a.kc + (long long)b * a.cb + (long long)kvh * a.ch;
+    const uint16_t* vb = a.vc + (long long)b * a.cb + (long long)kvh * a.ch;
+    auto load_k = [&](int kk, uint4* kr) {
+      const int key = min(kk + r, k1 - 1);
+      const uint16_t* p = kb + (long long)key * D + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[i] = ldg16_stream(p + 32 * i);
+    };
+    auto load_v = [&](int kk, uint4* vr) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int key = min(kk + g + 4 * s4, k1 - 1);
+        vr[s4] = ldg16_stream(vb + (long long)key * D + 8 * r);
+      }
+    };
+    uint4 ka[4], va[4], kb2[4], vb2[4];
+    if (active) {
+      load_k(k0, ka);
+      load_v(k0, va);
+    }
+
+    bf16x8 qa[4];
+    uint4 knew[4], vnew;
+    if constexpr (QKV) {
+      constexpr int NH = G / WM;  // q heads normed by each wavefront
+      const int nqkv = (nq + 2 * nkv) * D;
+      const int pt = min(max(pnew, 0), a.max_pos - 1);
+      const uint16_t* src = a.qkv + (long long)b * nqkv;
+      const bool do_k = new_unit && wave == 0;
+      uint32_t xh[NH], xk = 0, kwv = 0, vv = 0;
+#pragma unroll
+      for (int n = 0; n < NH; ++n)
+        xh[n] = reinterpret_cast<const uint32_t*>(src + (kvh * G + wave + n * WM) * D)[lane];
+      const uint32_t qwv = reinterpret_cast<const uint32_t*>(a.qw)[lane];
+      const uint32_t cwv = reinterpret_cast<const uint32_t*>(a.cosb + (long long)pt * D)[lane];
+      const uint32_t swv = reinterpret_cast<const uint32_t*>(a.sinb + (long long)pt * D)[lane];
+      if (do_k) {
+        xk = reinterpret_cast<const uint32_t*>(src + (nq + kvh) * D)[lane];
+        kwv = reinterpret_cast<const uint32_t*>(a.kw)[lane];
+        vv = reinterpret_cast<const uint32_t*>(src + (nq + nkv + kvh) * D)[lane];
+      }
+      if (has_new) vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
+      asm volatile("" ::: "memory");  // keep every load above ahead of the first wait
+#pragma unroll
+      for (int n = 0; n < NH; ++n) lds_q[wave + n * WM][lane] = norm_rope2(xh[n], qwv, cwv, swv, a.eps);
+      if (do_k) {
+        // the new key: to LDS for the wavefront that owns it, and the KV
+        // append at slot pnew (fused.py:88-96)
+        const uint32_t kn = norm_rope2(xk, kwv, cwv, swv, a.eps);
+        lds_k[lane] = kn;
+        const long long slot = (long long)b * a.cb + (long long)kvh * a.ch + (long long)pnew * D;
+        reinterpret_cast<uint32_t*>(a.kc + slot)[lane] = kn;
+        reinterpret_cast<uint32_t*>(a.vc + slot)[lane] = vv;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        qa[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&lds_q[r & 3][16 * i + 4 * g]));
+      if (has_new) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) knew[i] = *reinterpret_cast<const uint4*>(&lds_k[16 * i + 4 * g]);
+      }
+    } else {
+      const uint16_t* qrow = a.q + ((long long)b * nq + kvh * G + (r & 3)) * D + 8 * g;
+      uint4 qv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = ldg16(qrow + 32 * i);
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, qv[i]);
+    }
+
+    if (active) {
+      // kr / vr are consumed by this step, so the new key is patched in place.
+      auto step = [&](int kk, uint4 (&kr)[4], uint4 (&vr)[4]) {
+        if (QKV && has_new && kk <= pnew && pnew < kk + 16) {  // the new key: from registers
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (r == pnew - kk) kr[i] = knew[i];
+            // keys past pnew were clamped onto its (not yet written) slot:
+            // give them the new value too, so P = 0 never meets stale data
+            if (kk + g + 4 * i >= pnew) vr[i] = vnew;
+          }
+        }
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8, kr[i]),
+                                                       sc, 0, 0, 0);
+        const bool valid = (kk + r) < k1;
+        float sv[G];
+        bool need = false;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          sv[j] = valid ? sc[j] * a.scale_log2 : -INFINITY;
+          need |= sv[j] > mu[j] + TAU;
+        }
+        if (__ballot(need)) {
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            const float mn = fmaxf(mu[j], row_max16(sv[j]));
+            const float al = __builtin_amdgcn_exp2f(mu[j] - mn);
+            mu[j] = mn;
+            lsum[j] *= al;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[j][e] *= al;
+          }
+        }
+        float pf[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          pf[j] = __builtin_amdgcn_exp2f(sv[j] - mu[j]);
+          lsum[j] += pf[j];
+        }
+        const int pos = (r & 3) * 4 + (r >> 2);
+        const float pv = g == 0 ? pf[0] : g == 1 ? pf[1] : g == 2 ? pf[2] : pf[3];
+        myp[g * 16 + pos] = f32_to_bf16(pv);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        uint2 pw[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) pw[j] = *reinterpret_cast<const uint2*>(myp + j * 16 + 4 * g);
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) {
+          const uint32_t xs4[4] = {vr[2 * sp].x, vr[2 * sp].y, vr[2 * sp].z, vr[2 * sp].w};
+          const uint32_t ys4[4] = {vr[2 * sp + 1].x, vr[2 * sp + 1].y, vr[2 * sp + 1].z,
+                                   vr[2 * sp + 1].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = (xs4[e] & 0xffffu) | (ys4[e] << 16);
+            const uint32_t hi = (xs4[e] >> 16) | (ys4[e] & 0xffff0000u);
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+              const uint32_t pword = sp ? pw[j].y : pw[j].x;
+              acc[j][2 * e] = dot2_bf16(pword, lo, acc[j][2 * e]);
+              acc[j][2 * e + 1] = dot2_bf16(pword, hi, acc[j][2 * e + 1]);
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      };
+
+      if (k1 - k0 <= 16) {
+        step(k0, ka, va);  // one step: no prefetch
+      } else {
+        // Two-deep software pipeline over 16-key steps (loads clamp to k1 - 1,
+        // so they are unconditional and the wait counts stay exact).
+        for (int kk = k0; kk < k1; kk += 32) {
+          load_k(kk + 16, kb2);
+          load_v(kk + 16, vb2);
+          step(kk, ka, va);
+          if (kk + 16 >= k1) break;
+          load_k(kk + 32, ka);
+          load_v(kk + 32, va);
+          step(kk + 16, kb2, vb2);
+        }
+      }
+    }
+
+    // ---- merge the WM wavefront partials of the unit through LDS ----
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      float* dst = &lds_acc[wave][g][j][8 * r];
+      reinterpret_cast<float4*>(dst)[0] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+      reinterpret_cast<float4*>(dst)[1] = make_float4(acc[j][4], acc[j][5], acc[j][6], acc[j][7]);
+    }
+    float lrow[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) lrow[j] = row_sum16(lsum[j]);  // the 4 rows hold equal sums
+    if (lane < G) {
+      float m = mu[0], l = lrow[0];
+#pragma unroll
+      for (int j = 1; j < G; ++j) {
+        m = lane == j ? mu[j] : m;
+        l = lane == j ? lrow[j] : l;
+      }
+      lds_ml[wave][lane][0] = m;
+      lds_ml[wave][lane][1] = l;
+    }
+    __syncthreads();
+    {
+      constexpr int V = G * D / (64 * WM);  // outputs per thread
+      const int o0 = threadIdx.x * V;
+      const int j = o0 / D, d0 = o0 - j * D;
+      float Mx = NEG_BIG;
+#pragma unroll
+      for (int w = 0; w < WM; ++w) Mx = fmaxf(Mx, lds_ml[w][j][0]);
+      float L = 0.f, o[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[v] = 0.f;
+#pragma unroll
+      for (int w = 0; w < WM; ++w) {
+        const float sw = __builtin_amdgcn_exp2f(lds_ml[w][j][0] - Mx);
+        L += sw * lds_ml[w][j][1];
+        float t[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) t[v] = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+          for (int v = 0; v < V; ++v) t[v] += lds_acc[w][kg][j][d0 + v];
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] += sw * t[v];
+      }
+      const long long R = (long long)b * nq + kvh * G + j;
+      float* dst = a.o_part + (R * max_units + c) * D + d0;
+#pragma unroll
+      for (int v = 0; v < V; v += 2) reinterpret_cast<float2*>(dst + v)[0] = make_float2(o[v], o[v + 1]);
+      if (d0 == 0) reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(Mx, L);
+    }
+    __syncthreads();  // the next unit reuses the LDS
   }
 }
 
@@ -540,7 +850,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
   const int R = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (R >= rows) return;
   const int b = R / (T * nq);
-  combine_row(o_part, ml, R, -1, lens + b, len_off, cap, unit, max_units, out);
+  combine_row<64>(o_part, ml, R, -1, lens + b, len_off, cap, unit, max_units, out);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -568,10 +878,30 @@ int launch(const AttnArgs& a, int grid_waves, hipStream_t s) {
   return KO_LAUNCH_STATUS();
 }
 
+// Wavefronts per workgroup of attn1_kernel for a unit size: the largest of
+// 4, 2, 1 that splits the unit into whole 16-key steps.
+int waves_per_unit(int unit) { return unit % 64 == 0 ? 4 : unit % 32 == 0 ? 2 : 1; }
+
+template <bool QKV, int WM>
+int launch1_wm(const AttnArgs& a, int grid_waves, hipStream_t s) {
+  const dim3 grid((grid_waves + WM - 1) / WM), block(64 * WM);
+  hipLaunchKernelGGL((attn1_kernel<QKV, WM>), grid, block, 0, s, a);
+  return KO_LAUNCH_STATUS();
+}
+
+template <bool QKV>
+int launch1(const AttnArgs& a, int grid_waves, hipStream_t s) {
+  switch (waves_per_unit(a.unit)) {
+    case 4: return launch1_wm<QKV, 4>(a, grid_waves, s);
+    case 2: return launch1_wm<QKV, 2>(a, grid_waves, s);
+    default: return launch1_wm<QKV, 1>(a, grid_waves, s);
+  }
+}
+
 template <bool FUSED>
 int launch_t(const AttnArgs& a, int T, int grid_waves, hipStream_t s) {
   switch (T) {
-    case 1: return launch<1, false, FUSED>(a, grid_waves, s);
+    case 1: return FUSED ? launch<1, false, true>(a, grid_waves, s) : launch1<false>(a, grid_waves, s);
     case 2: return launch<2, false, FUSED>(a, grid_waves, s);
     case 3: return launch<3, false, FUSED>(a, grid_waves, s);
     default: return launch<4, false, FUSED>(a, grid_waves, s);
@@ -686,7 +1016,7 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
   a.out = static_cast<uint16_t*>(out);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (counters) return launch<1, true, true>(a, grid_waves, s);
-  st = launch<1, true, false>(a, grid_waves, s);
+  st = launch1<true>(a, grid_waves, s);
   if (st) return st;
   return ko_decode_attn_combine(o_part, ml, pos, 1, cap, B, 1, nkv * G, head_dim, unit,
                                 max_units, out, stream);

@@ -84,27 +84,55 @@ __device__ __forceinline__ float row_max16(float v) {
   v = fmaxf(v, dpp_f<0x121>(v));
   return v;
 }
-// Full 64-lane reductions (every lane ends with the total).
-__device__ __forceinline__ float wave_sum(float v) {
-  v = row_sum16(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+// Sums/maxima with the lane 16 or 32 places away (the xor-16 / xor-32
+// butterflies), on the VALU with the gfx950 permlane swaps instead of an LDS
+// permute. v_permlane16_swap(x, y) exchanges the odd rows of x with the even
+// rows of y; with x = y = v the two results hold v's rows {0, 0, 2, 2} and
+// {1, 1, 3, 3}, so their sum is v[i] + v[i ^ 16] in every lane.
+// v_permlane32_swap does the same with the two 32-lane halves.
+__device__ __forceinline__ float sum_xor16(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
 }
-__device__ __forceinline__ float wave_max(float v) {
-  v = row_max16(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+__device__ __forceinline__ float sum_xor32(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
 }
+__device__ __forceinline__ float max_xor16(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+}
+
+// Full 64-lane reductions (every lane ends with the total; call with all lanes
+// active).
+__device__ __forceinline__ float wave_sum(float v) { return sum_xor32(sum_xor16(row_sum16(v))); }
+__device__ __forceinline__ float wave_max(float v) { return max_xor32(max_xor16(row_max16(v))); }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+// Inclusive prefix sum over the 64 lanes (call with all lanes active):
+// Hillis-Steele inside each 16-lane row with DPP row_shr:1/2/4/8 (lanes whose
+// source falls outside the row read 0), then the totals of the rows below.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int t = __shfl_up(v, o, 64);
-    if (l >= o) v += t;
-  }
-  return v;
+  v += dpp_i<0x111>(v);
+  v += dpp_i<0x112>(v);
+  v += dpp_i<0x114>(v);
+  v += dpp_i<0x118>(v);
+  const int t0 = __builtin_amdgcn_readlane(v, 15);
+  const int t1 = __builtin_amdgcn_readlane(v, 31);
+  const int t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
 }
 
 __device__ __forceinline__ int readlane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }

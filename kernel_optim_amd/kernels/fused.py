@@ -60,11 +60,15 @@ class DecodeAttention:
     only valid keys are read and short sequences take few units. A fixed grid
     of ``grid_waves`` wavefronts strides over the units (graph-safe).
     ``target_ctas`` is the number of wavefronts to fill the GPU with
-    (256 CUs x 8 by default). A second launch merges the partials, as the
-    reference does; with ``fused_combine`` the last unit of each (sequence, KV
-    head) merges them in the same launch instead, through an arrival counter
-    and a device-scope fence per unit (slower on MI355X, where that fence
-    writes back the L2, so it is off by default).
+    (256 CUs x 8 by default). For one query token per sequence a unit is
+    shared by the 4 wavefronts of a workgroup (``unit / 4`` keys each, merged
+    in LDS), so the unit is 4x the per-wavefront share.
+
+    A second launch merges the partials, as the reference does; with
+    ``fused_combine`` the last unit of each (sequence, KV head) merges them in
+    the same launch instead, through an arrival counter and a device-scope
+    fence per unit (slower on MI355X, where that fence writes back the L2, so
+    it is off by default).
     """
 
     MAX_T = 4
@@ -75,13 +79,17 @@ class DecodeAttention:
         _need(nq == 4 * nkv, "the kernel serves GQA groups of 4 query heads per KV head")
         _need(1 <= T <= self.MAX_T, f"T must be in 1..{self.MAX_T}")
         self.B, self.T, self.cap, self.nq, self.nkv, self.d = B, T, cap, nq, nkv, d
+        wg_split = T == 1 and not fused_combine
         if unit is None:
-            unit = _cdiv(_cdiv(B * nkv * cap, target_ctas), 16) * 16
-            unit = max(64, min(1024, unit))
+            share = _cdiv(_cdiv(B * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
+            unit = 4 * max(16, min(1024, share)) if wg_split else max(64, min(1024, share))
         _need(unit % 16 == 0 and unit >= 16, "unit must be a positive multiple of 16")
         self.unit = unit
         self.max_units = _cdiv(cap, unit)
-        self.grid_waves = max(1, min(B * nkv * self.max_units, target_ctas))
+        # wavefronts per unit: the kernel's rule (attention.hip, waves_per_unit)
+        wpu = (4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1) if wg_split else 1
+        self.waves_per_unit = wpu
+        self.grid_waves = max(1, min(B * nkv * self.max_units * wpu, target_ctas))
         rows = B * T * nq
         self.o_part = torch.empty(rows * self.max_units * d, dtype=torch.float32, device=device)
         self.ml = torch.empty(rows * self.max_units * 2, dtype=torch.float32, device=device)

@@ -110,6 +110,17 @@ class Qwen3Oracle:
             toks.append(tok)
         return torch.stack(toks, 1), steps
 
+    def teacher_forced_decode(self, prompt, tokens):
+        """Decode-shaped replay of a given token sequence: the prompt in one forward,
+        then each of tokens[:, :-1] at its own position, one forward per token (the
+        shapes of Transformers' generate with a KV cache). Returns the logits at the
+        n generated positions, [B, n, V], on the CPU."""
+        S = prompt.shape[1]
+        out = [self.forward(prompt, 0)[:, -1].cpu()]
+        for j in range(1, tokens.shape[1]):
+            out.append(self.forward(tokens[:, j - 1:j], S + j - 1)[:, -1].cpu())
+        return torch.stack(out, 1)
+
     def teacher_forced(self, prompt, tokens):
         """Logits after the prompt and after each of tokens[:, :-1] (one forward
         over the whole sequence): [B, n, V] for the n generated positions."""

@@ -98,3 +98,36 @@ def test_two_generate_calls_do_not_share_state(dev):
     b = list(eng.generate(p2, 6))
     a2 = list(eng.generate(p1, 6))
     assert a == a2 and len(b) == 6 and all(len(x) == 2 for x in b)
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_engine_full_size_prompt1024_256_tokens(dev, B):
+    """The decode workload at full size: Qwen3-4B architecture (36 layers, random
+    N(0, 0.02) bf16 weights), prompts of 1024 seeded random ids, 256 greedy tokens.
+    The reference eager path replays the emitted tokens decode-shaped (one forward
+    per token, as generate() with a KV cache runs): every token must be within the
+    tie margin and the 2x-error rule. The prefill-shaped replay (one forward over
+    the whole sequence) measures the reference path's own bf16 rounding noise under
+    a change of GEMM shapes (ref_noise = max |decode-shaped - prefill-shaped|); the
+    engine's logits must be within max(LOGIT_ATOL, 1.5 * ref_noise) of the
+    decode-shaped replay: no further from the reference than the reference is from
+    itself, with half again as margin."""
+    cfg = Qwen3Config()
+    w = random_weights(cfg, seed=0, device=dev)
+    S, n = 1024, 256
+    prompt = torch.randint(0, cfg.vocab, (B, S), generator=torch.Generator().manual_seed(B))
+    eng = _engine(cfg, w)
+    toks, logits = eng.trace(prompt.tolist(), n)
+    del eng
+    torch.cuda.empty_cache()
+    orc = Qwen3Oracle(cfg, w, B=B, cap=S + n, device=dev)
+    replay = orc.teacher_forced_decode(prompt.to(dev), toks.to(dev))
+    prefill_shaped = orc.teacher_forced(prompt.to(dev), toks.to(dev)).cpu()
+    del orc
+    torch.cuda.empty_cache()
+    ref_noise = float((replay.float() - prefill_shaped.float()).abs().max())
+    agree, err = check_against_replay(toks, logits, replay)
+    agree_p = float((prefill_shaped.float().argmax(-1) == toks).float().mean())
+    print(f"full size B={B}: greedy agreement {agree:.4f} (prefill-shaped replay {agree_p:.4f}), "
+          f"max |dlogit| {err:.4f}; reference decode- vs prefill-shaped {ref_noise:.4f}")
+    assert err <= max(LOGIT_ATOL, 1.5 * ref_noise)
