@@ -151,7 +151,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     are captured in one graph and timed with events."""
     import torch
     from kernel_optim_amd.kernels.fused import DecodeAttention
-    from kernel_optim_amd.kernels.gemv import EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv
+    from kernel_optim_amd.kernels.gemv import EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, tile_weights
     from kernel_optim_amd.engine import _rope_tables
     from kernel_optim_amd.model import Qwen3Config, random_weights
     cfg = Qwen3Config(layers=nsets)
@@ -159,7 +159,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     w = random_weights(cfg, seed=1, device=dev)
     cap = ctx + 16
     cos, sin = _rope_tables(cap, cfg.head_dim, cfg.theta, dev)
-    res = {}
+    res, tiles = {}, {}
     for B in Bs:
         g = torch.Generator(device=dev).manual_seed(B)
         kc = [torch.randn(B, cfg.nkv, cap, cfg.head_dim, device=dev, generator=g).to(torch.bfloat16)
@@ -178,17 +178,23 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
                    o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
                    gu=Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
                    down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e))
-        for name, key in (("qkv", "qkv"), ("o", "o"), ("gu", "gu"), ("down", "down")):
-            ops[name].tune([l[key] for l in L], time.monotonic() + 20)
+        W = {}
+        for name in ("qkv", "o", "gu", "down"):
+            raw = [l[name] for l in L]
+            tiled = None
+            if any(c[0] == 2 for c in ops[name].candidates()):
+                tiled = tiles.setdefault(name, [tile_weights(w_, swiglu=name == "gu") for w_ in raw])
+            ops[name].tune(raw, time.monotonic() + 20, tiled=tiled)
+            W[name] = tiled if ops[name].cfg[0] == 2 else raw
 
         def layer(i):
             lw = L[i]
-            ops["qkv"](h, lw["qkv"], y=qkv, nw=lw["w_in"])
+            ops["qkv"](h, W["qkv"][i], y=qkv, nw=lw["w_in"])
             att.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i], att_out,
                            cfg.eps)
-            ops["o"](att_out, lw["o"], h=h)
-            ops["gu"](h, lw["gu"], y=act, nw=lw["w_post"])
-            ops["down"](act, lw["down"], h=h)
+            ops["o"](att_out, W["o"][i], h=h)
+            ops["gu"](h, W["gu"][i], y=act, nw=lw["w_post"])
+            ops["down"](act, W["down"][i], h=h)
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -336,6 +342,45 @@ def bench_attention(args):
     }
 
 
+def bench_attention_ragged(reps=20):
+    """Ragged decode attention: B=64, one query token per sequence, lengths
+    randint(128, 16385) (seed 3) over a cache padded to 16384 keys, N(0, 1) bf16
+    K/V. GB/s counts only the valid keys (4096 B per key over 8 KV heads x K and
+    V) plus q and out; the padded tail is never read."""
+    import torch
+    from kernel_optim_amd.kernels.fused import DecodeAttention
+    dev = torch.device("cuda:0")
+    Bg, cap = 64, 16384
+    lens = torch.randint(128, 16385, (Bg,), generator=torch.Generator().manual_seed(3),
+                         dtype=torch.int32)
+    g = torch.Generator(device=dev).manual_seed(4)
+    k = torch.randn(Bg, NKV, cap, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(Bg, NKV, cap, D, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(Bg, NQ * D, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    lens_d = lens.to(dev)
+    att = DecodeAttention(Bg, 1, cap, NQ, NKV, D, dev)
+    for _ in range(3):
+        att.with_lengths(q, k, v, lens_d, out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        att.with_lengths(q, k, v, lens_d, out)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = 4096 * int(lens.sum()) + 2 * Bg * NQ * D * 2
+    del k, v
+    torch.cuda.empty_cache()
+    return {"workload": "ragged GQA decode attention, B=64, lengths U[128, 16384] (seed 3), "
+                        "cache padded to 16384, 32q/8kv, d128, bf16, partial + LSE combine",
+            "us_per_call": round(us, 2), "valid_bytes": nbytes,
+            "gbs": round(nbytes / us / 1e3, 1),
+            "frac_of_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+            "unit_keys": att.unit, "grid_waves": att.grid_waves}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -359,6 +404,8 @@ def main():
             line["decode_b16"] = bench_decode(args, eng, B=16)
         del eng
         torch.cuda.empty_cache()
+    if not args.no_attn:
+        line["attention_ragged_b64"] = bench_attention_ragged()
     if args.layer:
         line["layer_2048"] = bench_layer()
     print(json.dumps(line), flush=True)

@@ -140,6 +140,11 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  * layout 0: each 256-thread workgroup owns `rows` (4 or 8) columns; any M.
  * layout 1: each wavefront owns `rows` (1, 2, 4) columns, `waves` (2, 4)
  *           wavefronts per workgroup; M <= 4 per launch slice.
+ * layout 2: MFMA 16-column tiles, M <= 16 per launch slice (rows padded with
+ *           zeros), K in {2560, 4096, 9728} (SWIGLU: 2560, 4096); a persistent
+ *           grid of 256 * `rows` (1, 2 or 4) workgroups. w must be in the tiled
+ *           layout written by ko_gemv_tile (for SWIGLU: the gate rows tiled,
+ *           then the up rows tiled, each padded to a multiple of 16 rows).
  * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
             float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
@@ -150,6 +155,14 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
  * launch configuration (a size, not a status; -1 for bad arguments). Helper of
  * ko_gemv, no reference counterpart. */
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
+
+/* Re-lays a row-major bf16 weight w [rows, K] into the tiled layout of ko_gemv
+ * layout 2: wt holds ceil(rows/16)*16*K elements; for row tile t and k step s
+ * (32 columns) the 1 KiB block at element ((t * K/32 + s) * 64 + l) * 8 holds,
+ * for l = 0..63, row 16 t + l % 16, columns 32 s + 8 (l / 16) .. + 7 (zeros past
+ * the last row). K % 32 == 0. A one-time transform at weight load; no reference
+ * counterpart (the reference's Triton GEMV reads its row-major weights). */
+int ko_gemv_tile(const void* w, void* wt, int rows, int K, void* stream);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,7 @@ SIGNATURES = {
                 _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _ll, _int, _int, _int, _int,
                 _int, _int, _int, _int, _int, _f, _c_void_p],
     "ko_gemv_argmax_scratch": [_int, _int, _int, _int],
+    "ko_gemv_tile": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
 }
 
 # Entry points whose return value is a size, not a status.

@@ -171,22 +171,45 @@ __device__ __forceinline__ void norm_rope_head(const uint4 (&x)[4], const uint4 
 // for up to NB slots at a time (every slot in bounds) together with the length,
 // so a merge of up to NB slots costs one memory round trip; slots >= n are
 // masked. Pass n >= 0 when it is known already (then len_ptr is unused).
-template <int NB>
+// 8-byte load; COHERENT reads at device scope (a relaxed agent-scope atomic
+// load: global_load ... sc1), for data another workgroup of the same launch
+// wrote with store_coherent.
+template <bool COHERENT>
+__device__ __forceinline__ float2 load2(const float* p) {
+  if constexpr (COHERENT) {
+    const unsigned long long u = __hip_atomic_load(
+        reinterpret_cast<unsigned long long*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+        __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(float2, u);
+  } else {
+    return *reinterpret_cast<const float2*>(p);
+  }
+}
+// 8-byte relaxed agent-scope atomic store (global_store ... sc1): written
+// through to the device coherence point, so a device-scope load elsewhere sees
+// it once this wave's s_waitcnt vmcnt(0) has passed.
+__device__ __forceinline__ void store_coherent(float* p, float2 v) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p),
+                     __builtin_bit_cast(unsigned long long, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NB, bool COHERENT = false>
 __device__ void combine_row(const float* __restrict__ o_part, const float* __restrict__ ml,
                             long long R, int n, const int* len_ptr, int len_off, int cap,
                             int unit, int max_units, uint16_t* __restrict__ out) {
   const int lane = lane_id();
-  const float2* mlr = reinterpret_cast<const float2*>(ml) + R * max_units;
+  const float* mlr = ml + 2 * R * max_units;
   const float* op = o_part + R * max_units * D + 2 * lane;
   float L = 0.f, o0 = 0.f, o1 = 0.f, M = NEG_BIG;
   static_assert(NB <= 64, "one (m, l) slot per lane");
   for (int c0 = 0; c0 < max_units; c0 += NB) {
     const int cn = min(NB, max_units - c0);
-    const float2 mlc = lane < cn ? mlr[c0 + lane] : make_float2(NEG_BIG, 0.f);
+    const float2 mlc = lane < cn ? load2<COHERENT>(mlr + 2 * (c0 + lane)) : make_float2(NEG_BIG, 0.f);
     float2 a[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j)
-      if (j < cn) a[j] = *reinterpret_cast<const float2*>(op + (long long)(c0 + j) * D);
+      if (j < cn) a[j] = load2<COHERENT>(op + (long long)(c0 + j) * D);
     if (n < 0) {
       int l = *len_ptr + len_off;
       n = nunits(l < cap ? l : cap, unit);
@@ -568,8 +591,9 @@ __device__ __forceinline__ uint32_t norm_rope2(uint32_t x, uint32_t w, uint32_t 
 //     the QK^T result holds the same 16 scores (the A rows are the 4 heads
 //     replicated), so the running max stays wave-uniform without cross-row
 //     traffic.
-template <bool QKV, int WM>
+template <bool QKV, int WM, bool FUSED>
 __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
+  __shared__ int lds_prev;
   __shared__ __align__(16) uint16_t lds_p[WM][G * 16];
   __shared__ __align__(16) float lds_acc[WM][4][G][D];  // [wave][key group g][head][col]
   __shared__ float lds_ml[WM][G][2];
@@ -834,9 +858,35 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
       }
       const long long R = (long long)b * nq + kvh * G + j;
       float* dst = a.o_part + (R * max_units + c) * D + d0;
+      if constexpr (FUSED) {
 #pragma unroll
-      for (int v = 0; v < V; v += 2) reinterpret_cast<float2*>(dst + v)[0] = make_float2(o[v], o[v + 1]);
-      if (d0 == 0) reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(Mx, L);
+        for (int v = 0; v < V; v += 2) store_coherent(dst + v, make_float2(o[v], o[v + 1]));
+        if (d0 == 0) store_coherent(a.ml + 2 * (R * max_units + c), make_float2(Mx, L));
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; v += 2)
+          reinterpret_cast<float2*>(dst + v)[0] = make_float2(o[v], o[v + 1]);
+        if (d0 == 0) reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(Mx, L);
+      }
+    }
+    if constexpr (FUSED) {
+      // Count the unit's arrival once every thread's partial stores are
+      // performed at device scope; the last unit of the (b, kv_head) pair to
+      // arrive merges the pair's partials with device-scope loads and re-arms
+      // the counter for the next launch. Nothing waits on another workgroup.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      int* ctr = a.counters + (long long)b * nkv + kvh;
+      if (threadIdx.x == 0)
+        lds_prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int n = nunits(kv_len, unit);
+      if (lds_prev == n - 1) {
+        for (int j = wave; j < G; j += WM)
+          combine_row<32, true>(a.o_part, a.ml, (long long)b * nq + kvh * G + j, n, nullptr, 0,
+                                a.cap, unit, max_units, a.out);
+        if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __syncthreads();  // the next unit reuses the LDS
   }
@@ -882,26 +932,26 @@ int launch(const AttnArgs& a, int grid_waves, hipStream_t s) {
 // 4, 2, 1 that splits the unit into whole 16-key steps.
 int waves_per_unit(int unit) { return unit % 64 == 0 ? 4 : unit % 32 == 0 ? 2 : 1; }
 
-template <bool QKV, int WM>
+template <bool QKV, int WM, bool FUSED>
 int launch1_wm(const AttnArgs& a, int grid_waves, hipStream_t s) {
   const dim3 grid((grid_waves + WM - 1) / WM), block(64 * WM);
-  hipLaunchKernelGGL((attn1_kernel<QKV, WM>), grid, block, 0, s, a);
+  hipLaunchKernelGGL((attn1_kernel<QKV, WM, FUSED>), grid, block, 0, s, a);
   return KO_LAUNCH_STATUS();
 }
 
-template <bool QKV>
+template <bool QKV, bool FUSED>
 int launch1(const AttnArgs& a, int grid_waves, hipStream_t s) {
   switch (waves_per_unit(a.unit)) {
-    case 4: return launch1_wm<QKV, 4>(a, grid_waves, s);
-    case 2: return launch1_wm<QKV, 2>(a, grid_waves, s);
-    default: return launch1_wm<QKV, 1>(a, grid_waves, s);
+    case 4: return launch1_wm<QKV, 4, FUSED>(a, grid_waves, s);
+    case 2: return launch1_wm<QKV, 2, FUSED>(a, grid_waves, s);
+    default: return launch1_wm<QKV, 1, FUSED>(a, grid_waves, s);
   }
 }
 
 template <bool FUSED>
 int launch_t(const AttnArgs& a, int T, int grid_waves, hipStream_t s) {
   switch (T) {
-    case 1: return FUSED ? launch<1, false, true>(a, grid_waves, s) : launch1<false>(a, grid_waves, s);
+    case 1: return launch1<false, FUSED>(a, grid_waves, s);
     case 2: return launch<2, false, FUSED>(a, grid_waves, s);
     case 3: return launch<3, false, FUSED>(a, grid_waves, s);
     default: return launch<4, false, FUSED>(a, grid_waves, s);
@@ -1015,8 +1065,8 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
   a.counters = counters;
   a.out = static_cast<uint16_t*>(out);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (counters) return launch<1, true, true>(a, grid_waves, s);
-  st = launch1<true>(a, grid_waves, s);
+  if (counters) return launch1<true, true>(a, grid_waves, s);
+  st = launch1<true, false>(a, grid_waves, s);
   if (st) return st;
   return ko_decode_attn_combine(o_part, ml, pos, 1, cap, B, 1, nkv * G, head_dim, unit,
                                 max_units, out, stream);

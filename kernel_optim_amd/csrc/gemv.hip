@@ -25,6 +25,21 @@
 //            normalised x through LDS, so the NORM prologue runs once per
 //            workgroup. Row counts are chosen so every CU gets the same number
 //            of rows (e.g. N=2560 -> 10 rows per CU). M <= 4.
+//   layout 2 "mfma" : for up to 16 rows of x the product is a real contraction:
+//            v_mfma_f32_16x16x32_bf16 with A = the (zero-padded) 16 rows of x and
+//            B = 16 weight rows, one MFMA per 1 KiB of weights. A workgroup of
+//            4 or 8 wavefronts owns a 16-column tile (plus the matching up tile
+//            for SWIGLU), each wavefront a slice of K; the partial tiles are
+//            summed through LDS and the epilogue runs one thread per (m, n).
+//            Workgroups are persistent over tiles and the weight loads of the
+//            next tile are issued during the last steps of the current one.
+//            Each wavefront keeps its K slice of x (normalised for NORM) in
+//            registers for all its tiles, so only weights stream. K is 2560
+//            (8 wavefronts x 10 steps), 4096 (8 x 16) or 9728 (8 x 38). The
+//            weights come in the tiled layout of ko_gemv_tile, in which every
+//            load instruction reads 1 KiB contiguous (the MFMA operand layout
+//            read from row-major weights touches 16 rows x 64 B per instruction
+//            and tops out near 5 TB/s on MI355X).
 #include "ko_common.h"
 
 using namespace ko;
@@ -418,6 +433,170 @@ __global__ __launch_bounds__(64 * WPB) void gemv_wave_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// layout 2: MFMA tiles of 16 columns, x rows padded to 16
+// ---------------------------------------------------------------------------
+constexpr int MFMA_CUS = 256;  // MI355X compute units: persistent grid = 256 x rows
+
+// Row-wise (16-lane) argmax of (value, index): lowest index on ties.
+__device__ __forceinline__ void row_argmax16(float& v, int& i) {
+#define KO_ARG_STEP(CTRL)                                                                  \
+  {                                                                                        \
+    const float ov = dpp_f<CTRL>(v);                                                       \
+    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xf, 0xf, false);               \
+    if (ov > v || (ov == v && oi < i)) {                                                   \
+      v = ov;                                                                              \
+      i = oi;                                                                              \
+    }                                                                                      \
+  }
+  KO_ARG_STEP(0x128)
+  KO_ARG_STEP(0x124)
+  KO_ARG_STEP(0x122)
+  KO_ARG_STEP(0x121)
+#undef KO_ARG_STEP
+}
+
+template <int EPI, bool NORM, int S, int PD, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int ntiles) {
+  static_assert(S % PD == 0, "the weight ring must tile the K steps");
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
+  __shared__ float s_c[WPG][NW][16][17];
+  __shared__ float s_sq[WPG][16];
+
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, mr = a.mrows;
+  const int kw0 = wv * (32 * S) + 8 * g;  // this lane's first k (step s adds 32 s)
+  const bool mok = col < mr;               // A row m = col exists
+
+  // Ring of PD weight steps in flight. The weights are in the tiled layout
+  // (ko_gemv_tile): the B operand of (tile, step) is one 1 KiB block with lane
+  // l's 16 bytes at 16 l, and a wavefront's steps are consecutive blocks.
+  const int T = (N + 15) / 16, KS = K / 32;
+  const uint16_t* wlane = a.w + (long long)(wv * S) * 512 + 8 * lane;
+  uint4 wb[PD][NW];
+  auto issue = [&](int tile, int s, int slot) {
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + s) * 512);
+  };
+  // The first tile's weights do not depend on x: issue them before the prologue.
+#pragma unroll
+  for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
+
+  // This wavefront's K slice of x (A operand, row m = col), kept in registers
+  // for every tile; NORM normalises it once.
+  bf16x8 xa[S];
+  {
+    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+    uint4 xr[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM) {
+      float rstd;
+      if (a.ss) {
+        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+      } else {
+        float sq = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) sq += sq8(xr[s]);
+        sq = sum_xor32(sum_xor16(sq));  // the 4 lane groups of row m
+        if (g == 0) s_sq[wv][col] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) tot += s_sq[w][col];
+        rstd = rsqrtf(tot / (float)K + a.eps);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], ldg16(a.nw + kw0 + 32 * s), rstd);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
+  }
+
+
+  float bv = -INFINITY;  // ARGMAX: running best of row t / 16 (threads with t % 16 == 0)
+  int bi = 0x7fffffff;
+  int tile = blockIdx.x;
+  for (; tile < ntiles; tile += gridDim.x) {
+    const int nxt = tile + gridDim.x < ntiles ? tile + gridDim.x : tile;  // clamp: loads stay valid
+    f32x4 c[NW];
+#pragma unroll
+    for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int slot = s % PD;
+#pragma unroll
+      for (int r = 0; r < NW; ++r)
+        c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
+                                                       c[r], 0, 0, 0);
+      if (s + PD < S) issue(tile, s + PD, slot);
+      else issue(nxt, s + PD - S, slot);  // the next tile's first steps
+    }
+    // C lane layout: column col, rows 4g + i.
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_c[wv][r][4 * g + i][col] = c[r][i];
+    __syncthreads();
+    if (t < 256) {
+      const int m = t >> 4, j = t & 15, n = tile * 16 + j;
+      float tot = 0.f, tot2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) {
+        tot += s_c[w][0][m][j];
+        if constexpr (NW == 2) tot2 += s_c[w][NW - 1][m][j];
+      }
+      const bool ok = m < mr && n < N;
+      float h2 = 0.f;
+      if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+      if constexpr (EPI == EPI_RESID) {
+        if (a.ss_out) {
+          h2 = row_sum16(h2);
+          if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+        }
+      }
+      if constexpr (EPI == EPI_ARGMAX) {
+        float v = ok ? round_bf16(tot) : -INFINITY;
+        int vi = ok ? n : 0x7fffffff;
+        row_argmax16(v, vi);
+        if (v > bv || (v == bv && vi < bi)) {
+          bv = v;
+          bi = vi;
+        }
+      }
+    }
+    __syncthreads();  // s_c is rewritten by the next tile
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    const int m = t >> 4;
+    if (t < 256 && (t & 15) == 0 && m < mr)
+      a.part[(long long)m * a.nparts + blockIdx.x] = make_float2(bv, __int_as_float(bi));
+  }
+}
+
+// Weight layout of layout 2 ("tiled"): rows padded to a multiple of 16; for
+// row tile t and k step s (32 columns) a 1 KiB block at ((t * K/32 + s) * 64 + l)
+// * 8 elements holds, for lane l, row 16 t + l % 16, columns 32 s + 8 (l / 16)
+// .. + 7 -- the v_mfma_f32_16x16x32_bf16 B-operand layout, so one 16-byte load
+// per lane reads the block contiguously.
+__global__ __launch_bounds__(256) void gemv_tile_kernel(const uint16_t* __restrict__ w,
+                                                        uint16_t* __restrict__ wt, int rows,
+                                                        int K, long long nchunks) {
+  const int KS = K / 32;
+  for (long long c = blockIdx.x * 256LL + threadIdx.x; c < nchunks; c += (long long)gridDim.x * 256) {
+    const int l = (int)(c & 63);
+    const long long blk = c >> 6;
+    const int s = (int)(blk % KS);
+    const long long t = blk / KS;
+    const long long row = t * 16 + (l & 15);
+    const int k = 32 * s + 8 * (l >> 4);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < rows) v = ldg16(w + row * K + k);
+    *reinterpret_cast<uint4*>(wt + c * 8) = v;
+  }
+}
+
 // One 1024-thread workgroup per row m: argmax over the work units' (value,
 // index) pairs with the lowest index on ties, loads issued 8 per thread at a
 // time. Optionally pos[m] += 1 (the decode step's position advance,
@@ -536,10 +715,61 @@ int launch_wave_cfg(const GemvArgs& a, int epi, bool norm, int rw, int wpb, hipS
   return KO_ENOTSUP;
 }
 
+int mfma_grid(int N, int per_cu) {
+  const int ntiles = (N + 15) / 16;
+  const int g = MFMA_CUS * per_cu;
+  return ntiles < g ? ntiles : g;
+}
+
+template <int S, int PD, int WPG>
+int launch_mfma_s(const GemvArgs& a, int epi, bool norm, int grid, hipStream_t s) {
+  const int ntiles = (a.N + 15) / 16;
+#define KO_M(NORMV, EPIV)                                                             \
+  hipLaunchKernelGGL((gemv_mfma_kernel<EPIV, NORMV, S, PD, WPG>), dim3(grid), dim3(64 * WPG), 0, \
+                     s, a, ntiles)
+  if (norm) {
+    switch (epi) {
+      case EPI_F32: KO_M(true, EPI_F32); break;
+      case EPI_BF16: KO_M(true, EPI_BF16); break;
+      case EPI_RESID: KO_M(true, EPI_RESID); break;
+      case EPI_SWIGLU: KO_M(true, EPI_SWIGLU); break;
+      default: KO_M(true, EPI_ARGMAX); break;
+    }
+  } else {
+    switch (epi) {
+      case EPI_F32: KO_M(false, EPI_F32); break;
+      case EPI_BF16: KO_M(false, EPI_BF16); break;
+      case EPI_RESID: KO_M(false, EPI_RESID); break;
+      case EPI_SWIGLU: KO_M(false, EPI_SWIGLU); break;
+      default: KO_M(false, EPI_ARGMAX); break;
+    }
+  }
+#undef KO_M
+  return KO_LAUNCH_STATUS();
+}
+
+// K = 32 * S * WPG: S steps of 32 per wavefront, WPG wavefronts splitting K.
+// SWIGLU (two weight tiles) needs K <= 4096 to keep its registers.
+bool mfma_supported(int K, int epi) {
+  return K == 2560 || K == 4096 || (K == 9728 && epi != EPI_SWIGLU);
+}
+
+int launch_mfma(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s) {
+  const int grid = mfma_grid(a.N, per_cu);
+  switch (a.K) {
+    case 2560: return launch_mfma_s<10, 10, 8>(a, epi, norm, grid, s);
+    case 4096: return launch_mfma_s<16, 16, 8>(a, epi, norm, grid, s);
+    default:
+      if (epi == EPI_SWIGLU) return KO_ENOTSUP;
+      return launch_mfma_s<38, 19, 8>(a, epi, norm, grid, s);
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 long long parts_for(int N, int layout, int rows, int waves) {
   if (layout == 0) return (N + rows - 1) / rows;
+  if (layout == 2) return mfma_grid(N, rows);
   const long long units = (N + rows - 1) / rows;
   return ((units + waves - 1) / waves) * waves;
 }
@@ -563,10 +793,13 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
   } else if (layout == 1) {
     if (M > 4) return KO_ENOTSUP;
     if (norm && (long long)M * K * 2 > LDS_X_BYTES) return KO_ENOTSUP;
+  } else if (layout == 2) {
+    if (rows != 1 && rows != 2 && rows != 4) return KO_ENOTSUP;
+    if (!mfma_supported(K, epi)) return KO_ENOTSUP;
   } else {
     return KO_EINVAL;
   }
-  const int mstep = layout == 0 ? 16 : 4;
+  const int mstep = layout == 1 ? 4 : 16;
   const long long nparts = parts_for(N, layout, rows, waves);
   if (epi == EPI_ARGMAX) {
     if (!ids || !part) return KO_EINVAL;
@@ -599,8 +832,10 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
     int st;
     if (layout == 0)
       st = rows == 4 ? launch_block_r<4>(a, epi, norm != 0, s) : launch_block_r<8>(a, epi, norm != 0, s);
-    else
+    else if (layout == 1)
       st = launch_wave_cfg(a, epi, norm != 0, rows, waves, s);
+    else
+      st = launch_mfma(a, epi, norm != 0, rows, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
       hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(FT), 0, s, a.part, a.nparts,
@@ -615,10 +850,22 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
   return KO_OK;
 }
 
+int ko_gemv_tile(const void* w, void* wt, int rows, int K, void* stream) {
+  if (!w || !wt || rows < 1 || K < 32 || (K % 32)) return KO_EINVAL;
+  if (!al16(w) || !al16(wt)) return KO_EINVAL;
+  const long long nchunks = (long long)((rows + 15) / 16) * 16 * (K / 8);
+  long long blocks = (nchunks + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(gemv_tile_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w),
+                     static_cast<uint16_t*>(wt), rows, K, nchunks);
+  return KO_LAUNCH_STATUS();
+}
+
 // fp32 scratch elements ko_gemv needs for EPI 4 (ARGMAX) with this layout
 // (a size, not a status; -1 for bad arguments).
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
-  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 1) return -1;
+  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 2) return -1;
   return 2LL * 16 * parts_for(N, layout, rows, waves);
 }
 

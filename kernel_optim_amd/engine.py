@@ -33,7 +33,7 @@ import time
 import torch
 
 from .kernels.fused import DecodeAttention
-from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss
+from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss, tile_weights
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
 
@@ -92,6 +92,7 @@ class Engine:
         self._cos = self._sin = None
         self._shape = None
         self.g1 = None
+        self._tile_cache = {}
 
     # ------------------------------------------------------------------ setup
     def _tables(self, n):
@@ -127,37 +128,51 @@ class Engine:
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
         H, L = cfg.hidden, self.w["layers"]
+        e = cfg.eps
         self.gv = dict(
-            qkv=(Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=cfg.eps), [l["qkv"] for l in L]),
-            o=(Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=cfg.eps),
-               [l["o"] for l in L]),
-            gu=(Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=cfg.eps), [l["gu"] for l in L]),
-            down=(Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=cfg.eps),
-                  [l["down"] for l in L]),
-            lm=(Gemv(B, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=cfg.eps), [self.w["lm_head"]]),
+            qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
+            o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
+            gu=Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
+            down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e),
+            lm=Gemv(B, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
         )
-        if TUNE:
-            deadline = time.monotonic() + TUNE_BUDGET_S
-            for name, (g, ws) in self.gv.items():
-                g.tune(ws, deadline)
+        raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],
+                   down=[l["down"] for l in L], lm=[self.w["lm_head"]])
+        deadline = time.monotonic() + TUNE_BUDGET_S
+        self.gw = {}
+        for name, g in self.gv.items():
+            tiled = None
+            if any(c[0] == 2 for c in g.candidates()):
+                tiled = self._tiled(name, raw[name])
+            if TUNE:
+                g.tune(raw[name], deadline, tiled=tiled)
                 _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
+            self.gw[name] = tiled if g.cfg[0] == 2 else raw[name]
         self.g1 = self._capture(self._step1)
         self._shape = key
+
+    def _tiled(self, name, weights):
+        """MFMA-layout copies of one projection's weights (kernels.gemv.tile_weights),
+        made once and kept for every later batch size that uses them."""
+        if name not in self._tile_cache:
+            self._tile_cache[name] = [tile_weights(w, swiglu=name == "gu") for w in weights]
+            torch.cuda.synchronize()
+        return self._tile_cache[name]
 
     def _step1(self):
         """One decode token per sequence at pos[b]; greedy ids; positions advance."""
         cfg = self.cfg
-        g = {k: v[0] for k, v in self.gv.items()}
+        g, W = self.gv, self.gw  # W: each projection's weights in its launch layout
         h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
         for i, lw in enumerate(self.w["layers"]):
-            g["qkv"](h, lw["qkv"], y=self.qkv, nw=lw["w_in"])
+            g["qkv"](h, W["qkv"][i], y=self.qkv, nw=lw["w_in"])
             self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
                                  self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
                                  cfg.eps)
-            g["o"](self.attn_out, lw["o"], h=h)
-            g["gu"](h, lw["gu"], y=self.act, nw=lw["w_post"])
-            g["down"](self.act, lw["down"], h=h)
-        g["lm"](h, self.w["lm_head"], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
+            g["o"](self.attn_out, W["o"][i], h=h)
+            g["gu"](h, W["gu"][i], y=self.act, nw=lw["w_post"])
+            g["down"](self.act, W["down"][i], h=h)
+        g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
                 pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
 
     def _capture(self, fn):

@@ -66,9 +66,10 @@ class DecodeAttention:
 
     A second launch merges the partials, as the reference does; with
     ``fused_combine`` the last unit of each (sequence, KV head) merges them in
-    the same launch instead, through an arrival counter and a device-scope
-    fence per unit (slower on MI355X, where that fence writes back the L2, so
-    it is off by default).
+    the same launch instead, through an arrival counter. For one query token
+    the partials travel through device-coherent stores and loads (no L2
+    write-back); for T > 1 a device-scope fence per unit publishes them, which
+    costs an L2 write-back on MI355X.
     """
 
     MAX_T = 4
@@ -79,7 +80,7 @@ class DecodeAttention:
         _need(nq == 4 * nkv, "the kernel serves GQA groups of 4 query heads per KV head")
         _need(1 <= T <= self.MAX_T, f"T must be in 1..{self.MAX_T}")
         self.B, self.T, self.cap, self.nq, self.nkv, self.d = B, T, cap, nq, nkv, d
-        wg_split = T == 1 and not fused_combine
+        wg_split = T == 1
         if unit is None:
             share = _cdiv(_cdiv(B * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
             unit = 4 * max(16, min(1024, share)) if wg_split else max(64, min(1024, share))

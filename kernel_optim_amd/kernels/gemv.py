@@ -29,7 +29,7 @@ import time
 import torch
 
 from .. import _lib
-from .fused import BF16, _check, _need
+from .fused import BF16, _cdiv, _check, _need
 
 EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3, 4
 
@@ -47,18 +47,28 @@ class Gemv:
         self._part = None
         self.us = float("nan")
 
+    def mfma_ok(self):
+        """Layout 2 (MFMA tiles, x rows padded to 16) takes K in {2560, 4096, 9728},
+        SWIGLU only up to 4096 (gemv.hip, mfma_supported)."""
+        return self.K in (2560, 4096) or (self.K == 9728 and self.epi != EPI_SWIGLU)
+
     def candidates(self):
         """Launch configurations, the default first. Layout 1 (a wavefront per row
         group) is the batch-1..4 path; layout 0 serves every batch up to 16 rows
-        per launch."""
+        per launch with VALU dot products; layout 2 puts 2..16 rows on MFMA
+        (``(2, per_cu, 0)``: a persistent grid of 256 x per_cu workgroups)."""
         out = []
+        mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
+        if self.M > 4:
+            out += mfma
+            mfma = []
         if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):
             per_wave = (4, 2, 1) if self.N >= 32768 else (1, 2, 4)
             for rows in per_wave:
                 for waves in (2, 4):
                     out.append((1, rows, waves))
         out += [(0, 4, 0), (0, 8, 0)] if self.N < 32768 else [(0, 8, 0), (0, 4, 0)]
-        return out
+        return out + mfma
 
     def _scratch(self, device, cfg):
         n = _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg)
@@ -74,7 +84,8 @@ class Gemv:
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
-        _check(w, "w", BF16, ((2 * N) if epi == EPI_SWIGLU else N, K))
+        nrows = _cdiv(N, 16) * 16 if layout == 2 else N  # layout 2: tile_weights copy
+        _check(w, "w", BF16, ((2 * nrows) if epi == EPI_SWIGLU else nrows, K))
         if self.norm:
             _check(nw, "nw", BF16, (K,))
             if ss is not None:
@@ -105,9 +116,11 @@ class Gemv:
                   0 if part is None else part.numel(), M, N, K, epi, int(self.norm), 0, layout,
                   rows, waves, self.eps, _lib.stream_ptr())
 
-    def tune(self, weights, deadline):
+    def tune(self, weights, deadline, tiled=None):
         """Pick the fastest candidate by GPU time: one call per layer weight (cold),
-        captured in a graph and replayed twice (gemv.py:152-195)."""
+        captured in a graph and replayed twice (gemv.py:152-195). Layout-2
+        candidates run on ``tiled`` (the tile_weights copies of ``weights``) and
+        are skipped without it."""
         dev = weights[0].device
         M, N, K = self.M, self.N, self.K
         x = torch.randn(M, K, device=dev, dtype=BF16)
@@ -121,12 +134,15 @@ class Gemv:
         for cfg in self.candidates():
             if time.monotonic() > deadline:
                 break
+            ws = tiled if cfg[0] == 2 else weights
+            if ws is None:
+                continue
             try:
-                self(x, weights[0], cfg=cfg, **kw)
+                self(x, ws[0], cfg=cfg, **kw)
                 torch.cuda.synchronize()
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
-                    for wt in weights:
+                    for wt in ws:
                         self(x, wt, cfg=cfg, **kw)
                 g.replay()
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -147,6 +163,26 @@ class Gemv:
             self.cfg = best[1]
             self.us = best[0] / (2 * len(weights)) * 1e3
         return self.cfg
+
+
+def tile_weights(w, swiglu=False):
+    """The layout-2 (MFMA) copy of a row-major bf16 weight: [N, K] -> [ceil(N/16)*16, K]
+    in the tiled order of ko_gemv_tile (one 1 KiB block per 16-row tile and 32-column
+    step, in the MFMA B-operand lane order). For SWIGLU ([2N, K], gate | up) the gate
+    and up halves are tiled separately. A one-time transform on the current stream."""
+    _check(w, "w", BF16)
+    _need(w.dim() == 2 and w.shape[1] % 32 == 0, "w must be [rows, K] with K % 32 == 0")
+    R, K = w.shape
+    halves = [w[: R // 2], w[R // 2:]] if swiglu else [w]
+    if swiglu:
+        _need(R % 2 == 0, "a SWIGLU weight has 2N rows")
+    n = halves[0].shape[0]
+    npad = _cdiv(n, 16) * 16
+    out = torch.empty(npad * len(halves), K, dtype=BF16, device=w.device)
+    for i, part in enumerate(halves):
+        _lib.call("ko_gemv_tile", _lib.ptr(part), _lib.ptr(out[i * npad:(i + 1) * npad]), n, K,
+                  _lib.stream_ptr())
+    return out
 
 
 def embed_ss(ids, emb, h, ss):

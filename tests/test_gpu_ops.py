@@ -124,7 +124,7 @@ def _weights(dev, N, K, seed, rows=None):
     return (0.02 * torch.randn(rows or N, K, device=dev, generator=g)).to(BF)
 
 
-CFGS = [(0, 4, 0), (0, 8, 0), (1, 1, 2), (1, 2, 4), (1, 4, 2)]
+CFGS = [(0, 4, 0), (0, 8, 0), (1, 1, 2), (1, 2, 4), (1, 4, 2), (2, 1, 0), (2, 2, 0)]
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 16])
@@ -134,6 +134,10 @@ def test_gemv_epilogues(dev, M, cfg):
     if cfg[0] == 1 and M > 4:
         pytest.skip("layout 1 serves M <= 4")
     rows = cfg
+
+    def lay(W, swiglu=False):  # layout 2 reads the tiled copy of the weights
+        return gemv.tile_weights(W, swiglu=swiglu) if cfg[0] == 2 else W
+
     g = _g(dev, 10 + M)
     # qkv: NORM + F32, ss computed in-kernel and passed explicitly
     N, Kd = SHAPES["qkv"]
@@ -144,7 +148,7 @@ def test_gemv_epilogues(dev, M, cfg):
     want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32, nw=nw.cpu(), ss=ss.cpu())
     for ss_arg in (None, ss):
         y = torch.empty(M, N, device=dev)
-        gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)(x, W, y=y, nw=nw, ss=ss_arg, cfg=rows)
+        gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)(x, lay(W), y=y, nw=nw, ss=ss_arg, cfg=rows)
         torch.cuda.synchronize()
         torch.testing.assert_close(y.cpu(), want, rtol=2e-3, atol=2e-3)
     # o: RESID with ss_out
@@ -154,7 +158,7 @@ def test_gemv_epilogues(dev, M, cfg):
     h = torch.randn(M, N, device=dev, generator=g).to(BF)
     hr, ssr = O.gemv(a.cpu(), W.cpu(), O.EPI_RESID, h=h.cpu())
     ss_out = torch.full((M,), 5.0, device=dev)
-    gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)(a, W, h=h, ss_out=ss_out, cfg=rows)
+    gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)(a, lay(W), h=h, ss_out=ss_out, cfg=rows)
     torch.cuda.synchronize()
     assert_bf16_close(h.cpu(), hr, max_frac=0.02, atol=one_ulp_at(hr))
     torch.testing.assert_close(ss_out.cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
@@ -163,7 +167,7 @@ def test_gemv_epilogues(dev, M, cfg):
     x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
     W = _weights(dev, N, Kd, 22, rows=2 * N)
     y = torch.empty(M, N, device=dev, dtype=BF)
-    gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)(x, W, y=y, nw=nw, cfg=rows)
+    gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)(x, lay(W, swiglu=True), y=y, nw=nw, cfg=rows)
     torch.cuda.synchronize()
     want = O.gemv(x.cpu(), W.cpu(), O.EPI_SWIGLU, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
     assert_bf16_close(y.cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
@@ -172,13 +176,14 @@ def test_gemv_epilogues(dev, M, cfg):
     a = torch.randn(M, Kd, device=dev, generator=g).to(BF)
     W = _weights(dev, N, Kd, 23)
     y = torch.empty(M, N, device=dev, dtype=BF)
-    gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)(a, W, y=y, cfg=rows)
+    gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)(a, lay(W), y=y, cfg=rows)
     torch.cuda.synchronize()
     want = O.gemv(a.cpu(), W.cpu(), O.EPI_BF16)
     assert_bf16_close(y.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
 
 
-@pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (16, (0, 8, 0))])
+@pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (16, (0, 8, 0)),
+                                   (3, (2, 1, 0)), (16, (2, 2, 0))])
 def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     _, gemv = K()
     V, H = 151936, 2560
@@ -188,11 +193,12 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     nw = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(BF)
     op = gemv.Gemv(M, V, H, gemv.EPI_ARGMAX, norm=True)
     op.cfg = cfg
+    Ew = gemv.tile_weights(E) if cfg[0] == 2 else E  # the GEMV's copy; E stays the table
     logits = torch.empty(M, V, device=dev, dtype=BF)
     ids = torch.empty(M, device=dev, dtype=torch.int64)
     pos = torch.arange(M, device=dev, dtype=torch.int32)
     nxt = torch.zeros(M, H, device=dev, dtype=BF)
-    op(x, E, y=logits, nw=nw, ids=ids, pos_inc=pos, next_emb=E, next_h=nxt)
+    op(x, Ew, y=logits, nw=nw, ids=ids, pos_inc=pos, next_emb=E, next_h=nxt)
     torch.cuda.synchronize()
     assert torch.equal(pos.cpu(), torch.arange(M, dtype=torch.int32) + 1)
     assert torch.equal(nxt, E[ids])
@@ -210,16 +216,38 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        op(x, E, nw=nw, ids=ids2)
+        op(x, Ew, nw=nw, ids=ids2)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     with torch.cuda.graph(g2):
-        op(x, E, nw=nw, ids=ids2)
+        op(x, Ew, nw=nw, ids=ids2)
     for _ in range(3):
         ids2.zero_()
         g2.replay()
         torch.cuda.synchronize()
         assert torch.equal(ids2, ids)
+
+
+@pytest.mark.parametrize("rows,swiglu", [(37, False), (64, True)])
+def test_tile_weights_layout(dev, rows, swiglu):
+    """ko_gemv_tile against the layout written out with torch: rows padded to 16,
+    then [tile][32-column step][k group][row in tile][8 columns]."""
+    _, gemv = K()
+    Kd = 96
+    W = torch.randn(rows, Kd, device=dev, generator=_g(dev, 40)).to(BF)
+    got = gemv.tile_weights(W, swiglu=swiglu)
+
+    def ref(part):
+        n = part.shape[0]
+        npad = -(-n // 16) * 16
+        p = torch.zeros(npad, Kd, dtype=BF)
+        p[:n] = part.cpu()
+        return p.view(npad // 16, 16, Kd // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(npad, Kd)
+
+    halves = [W[: rows // 2], W[rows // 2:]] if swiglu else [W]
+    want = torch.cat([ref(h) for h in halves])
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)
 
 
 def test_gemv_rejects_bad_shapes(dev):
