@@ -137,7 +137,8 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *              next_h[m] = next_emb[ids[m]] ([N, K] table) when both are given
  *              (the next step's embedding gather, gemv.py:201-211);
  *              part: fp32 scratch of part_len >= ko_gemv_argmax_scratch(...).
- * layout 0: each 256-thread workgroup owns `rows` (4 or 8) columns; any M.
+ * layout 0: each 256-thread workgroup owns `rows` (4 or 8; 16 when M <= 2)
+ *           columns; any M.
  * layout 1: each wavefront owns `rows` (1, 2, 4) columns, `waves` (2, 4)
  *           wavefronts per workgroup; M <= 4 per launch slice.
  * layout 2: MFMA 16-column tiles, M <= 16 per launch slice (rows padded with

@@ -34,6 +34,8 @@
 //           counter) merges the pair's partials and writes the bf16 output,
 //           so no second launch is needed; it re-arms the counter for the
 //           next launch.
+#include <type_traits>
+
 #include "ko_common.h"
 
 using namespace ko;
@@ -724,7 +726,10 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
 
     if (active) {
       // kr / vr are consumed by this step, so the new key is patched in place.
-      auto step = [&](int kk, uint4 (&kr)[4], uint4 (&vr)[4]) {
+      // FIRST (the wavefront's first step, with acc = l = 0 and no running max
+      // yet) sets the max from the step's scores instead of rescaling.
+      auto step = [&](int kk, uint4 (&kr)[4], uint4 (&vr)[4], auto first_tag) {
+        constexpr bool FIRST = decltype(first_tag)::value;
         if (QKV && has_new && kk <= pnew && pnew < kk + 16) {  // the new key: from registers
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -741,28 +746,33 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
                                                        sc, 0, 0, 0);
         const bool valid = (kk + r) < k1;
         float sv[G];
-        bool need = false;
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-          sv[j] = valid ? sc[j] * a.scale_log2 : -INFINITY;
-          need |= sv[j] > mu[j] + TAU;
-        }
-        if (__ballot(need)) {
+        for (int j = 0; j < G; ++j) sv[j] = valid ? sc[j] * a.scale_log2 : -INFINITY;
+        if constexpr (FIRST) {
+          // key kk is valid, so every row max is finite
 #pragma unroll
-          for (int j = 0; j < G; ++j) {
-            const float mn = fmaxf(mu[j], row_max16(sv[j]));
-            const float al = __builtin_amdgcn_exp2f(mu[j] - mn);
-            mu[j] = mn;
-            lsum[j] *= al;
+          for (int j = 0; j < G; ++j) mu[j] = row_max16(sv[j]);
+        } else {
+          bool need = false;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[j][e] *= al;
+          for (int j = 0; j < G; ++j) need |= sv[j] > mu[j] + TAU;
+          if (__ballot(need)) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+              const float mn = fmaxf(mu[j], row_max16(sv[j]));
+              const float al = __builtin_amdgcn_exp2f(mu[j] - mn);
+              mu[j] = mn;
+              lsum[j] *= al;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc[j][e] *= al;
+            }
           }
         }
         float pf[G];
 #pragma unroll
         for (int j = 0; j < G; ++j) {
           pf[j] = __builtin_amdgcn_exp2f(sv[j] - mu[j]);
-          lsum[j] += pf[j];
+          lsum[j] = FIRST ? pf[j] : lsum[j] + pf[j];
         }
         const int pos = (r & 3) * 4 + (r >> 2);
         const float pv = g == 0 ? pf[0] : g == 1 ? pf[1] : g == 2 ? pf[2] : pf[3];
@@ -780,13 +790,15 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
                                    vr[2 * sp + 1].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = (xs4[e] & 0xffffu) | (ys4[e] << 16);
-            const uint32_t hi = (xs4[e] >> 16) | (ys4[e] & 0xffff0000u);
+            // (x.lo16, y.lo16) and (x.hi16, y.hi16) with one v_perm_b32 each
+            const uint32_t lo = __builtin_amdgcn_perm(ys4[e], xs4[e], 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(ys4[e], xs4[e], 0x07060302u);
 #pragma unroll
             for (int j = 0; j < G; ++j) {
               const uint32_t pword = sp ? pw[j].y : pw[j].x;
-              acc[j][2 * e] = dot2_bf16(pword, lo, acc[j][2 * e]);
-              acc[j][2 * e + 1] = dot2_bf16(pword, hi, acc[j][2 * e + 1]);
+              const bool zero = FIRST && sp == 0;  // the first products start the sums
+              acc[j][2 * e] = dot2_bf16(pword, lo, zero ? 0.f : acc[j][2 * e]);
+              acc[j][2 * e + 1] = dot2_bf16(pword, hi, zero ? 0.f : acc[j][2 * e + 1]);
             }
           }
         }
@@ -794,19 +806,25 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
         __builtin_amdgcn_wave_barrier();
       };
 
+      using First = std::integral_constant<bool, true>;
+      using Next = std::integral_constant<bool, false>;
       if (k1 - k0 <= 16) {
-        step(k0, ka, va);  // one step: no prefetch
+        step(k0, ka, va, First{});  // one step: no prefetch
       } else {
         // Two-deep software pipeline over 16-key steps (loads clamp to k1 - 1,
         // so they are unconditional and the wait counts stay exact).
+        load_k(k0 + 16, kb2);
+        load_v(k0 + 16, vb2);
+        step(k0, ka, va, First{});
         for (int kk = k0; kk < k1; kk += 32) {
-          load_k(kk + 16, kb2);
-          load_v(kk + 16, vb2);
-          step(kk, ka, va);
           if (kk + 16 >= k1) break;
           load_k(kk + 32, ka);
           load_v(kk + 32, va);
-          step(kk + 16, kb2, vb2);
+          step(kk + 16, kb2, vb2, Next{});
+          if (kk + 32 >= k1) break;
+          load_k(kk + 48, kb2);
+          load_v(kk + 48, vb2);
+          step(kk + 32, ka, va, Next{});
         }
       }
     }

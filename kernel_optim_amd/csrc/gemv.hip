@@ -18,8 +18,9 @@
 //
 // Two mappings of rows to the machine (both stream each weight row with
 // coalesced 16-byte loads and accumulate with v_dot2c_f32_bf16):
-//   layout 0 "block": a 256-thread workgroup owns R output columns over the
-//            full K; thread t reads chunks t, t+256, ...; M <= 16.
+//   layout 0 "block": a 256-thread workgroup owns R (4, 8; 16 for M <= 2)
+//            output columns over the full K; thread t reads chunks t, t+256, ...;
+//            M <= 16.
 //   layout 1 "wave" : a wavefront owns RW output columns over the full K (lane l
 //            reads chunks l, l+64, ...); WPB wavefronts per workgroup share the
 //            normalised x through LDS, so the NORM prologue runs once per
@@ -681,6 +682,13 @@ int launch_block_r(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
   return launch_block<16, R>(a, epi, norm, s);
 }
 
+// 16 columns per workgroup (fewer ARGMAX partials for the finalize) for 1-2 rows.
+int launch_block_r16(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  if (a.mrows <= 1) return launch_block<1, 16>(a, epi, norm, s);
+  if (a.mrows <= 2) return launch_block<2, 16>(a, epi, norm, s);
+  return KO_ENOTSUP;
+}
+
 template <int M, int RW, int WPB>
 int launch_wave(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
   const int units = (a.N + RW - 1) / RW;
@@ -789,7 +797,7 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
   if ((epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_SWIGLU) && !y) return KO_EINVAL;
   if (epi == EPI_RESID && !h) return KO_EINVAL;
   if (layout == 0) {
-    if (rows != 4 && rows != 8) return KO_ENOTSUP;
+    if (rows != 4 && rows != 8 && !(rows == 16 && M <= 2)) return KO_ENOTSUP;
   } else if (layout == 1) {
     if (M > 4) return KO_ENOTSUP;
     if (norm && (long long)M * K * 2 > LDS_X_BYTES) return KO_ENOTSUP;
@@ -831,7 +839,9 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
     a.accumulate = accumulate;
     int st;
     if (layout == 0)
-      st = rows == 4 ? launch_block_r<4>(a, epi, norm != 0, s) : launch_block_r<8>(a, epi, norm != 0, s);
+      st = rows == 4   ? launch_block_r<4>(a, epi, norm != 0, s)
+           : rows == 8 ? launch_block_r<8>(a, epi, norm != 0, s)
+                       : launch_block_r16(a, epi, norm != 0, s);
     else if (layout == 1)
       st = launch_wave_cfg(a, epi, norm != 0, rows, waves, s);
     else

@@ -126,7 +126,7 @@ class Engine:
                        else None)
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
-        self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
+        self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
         H, L = cfg.hidden, self.w["layers"]
         e = cfg.eps
         self.gv = dict(

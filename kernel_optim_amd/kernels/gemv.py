@@ -68,6 +68,8 @@ class Gemv:
                 for waves in (2, 4):
                     out.append((1, rows, waves))
         out += [(0, 4, 0), (0, 8, 0)] if self.N < 32768 else [(0, 8, 0), (0, 4, 0)]
+        if self.M <= 2 and self.N >= 32768:
+            out.append((0, 16, 0))  # fewer ARGMAX partials
         return out + mfma
 
     def _scratch(self, device, cfg):
