@@ -269,6 +269,141 @@ __global__ __launch_bounds__(NT) void gemv_block_kernel(GemvArgs a) {
   }
 }
 
+// layout 0 for 1-2 rows of x: the same mapping with the load order arranged
+// for the memory system. x (and the NORM gain) are loaded first and kept in
+// registers (normalised once), then every weight chunk of the workgroup is
+// issued; loads return in issue order, so a dot product never waits behind a
+// later load. Chunk indices past K are clamped to a valid chunk whose x is
+// zeroed, which keeps the loads unconditional and the wait counts exact.
+// CPT = chunks of 8 per thread (K <= 2048 * CPT).
+template <int M, int R, bool NORM, int EPI, int CPT>
+__global__ __launch_bounds__(NT) void gemv_row_kernel(GemvArgs a) {
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 * R : R;
+  __shared__ float red[16][M * NW];
+  __shared__ float s_sq[NT / 64][M];
+  __shared__ float s_h2[M * R];
+  __shared__ float2 s_best[M * R];
+
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int n0 = blockIdx.x * R;
+  const int N = a.N, K = a.K, KC = K >> 3, mr = a.mrows;
+
+  uint4 xr[M][CPT];
+  uint4 nwr[NORM ? CPT : 1];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = min(t + NT * j, KC - 1);
+#pragma unroll
+    for (int m = 0; m < M; ++m) xr[m][j] = ldg16(a.x + (long long)(m < mr ? m : 0) * K + 8 * c);
+    if constexpr (NORM) nwr[j] = ldg16(a.nw + 8 * c);
+  }
+  uint4 w[CPT][NW];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = min(t + NT * j, KC - 1);
+#pragma unroll
+    for (int r = 0; r < NW; ++r) {
+      const int n = r < R ? min(n0 + r, N - 1) : N + min(n0 + r - R, N - 1);
+      w[j][r] = ldg16_stream(a.w + (long long)n * K + 8 * c);
+    }
+  }
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (t + NT * j >= KC || m >= mr) xr[m][j] = zero;
+
+  if constexpr (NORM) {
+    float rstd[M];
+    if (a.ss) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) rstd[m] = m < mr ? rsqrtf(a.ss[m] / (float)K + a.eps) : 0.f;
+    } else {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float sq = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) sq += sq8(xr[m][j]);
+        sq = wave_sum(sq);
+        if (lane == 0) s_sq[wv][m] = sq;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NT / 64; ++i) tot += s_sq[i][m];
+        rstd[m] = rsqrtf(tot / (float)K + a.eps);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+      for (int m = 0; m < M; ++m) xr[m][j] = norm8(xr[m][j], nwr[j], rstd[m]);
+  }
+
+  float acc[M][NW];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < NW; ++r) acc[m][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < NW; ++r) acc[m][r] = dot8(xr[m][j], w[j][r], acc[m][r]);
+
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < NW; ++r) {
+      const float v = row_sum16(acc[m][r]);
+      if ((lane & 15) == 0) red[wv * 4 + (lane >> 4)][m * NW + r] = v;
+    }
+  __syncthreads();
+
+  for (int idx = t; idx < M * R; idx += NT) {
+    const int m = idx / R, r = idx - (idx / R) * R, n = n0 + r;
+    float tot = 0.f, tot2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      tot += red[i][m * NW + r];
+      if constexpr (EPI == EPI_SWIGLU) tot2 += red[i][m * NW + R + r];
+    }
+    const bool ok = m < mr && n < N;
+    float h2 = 0.f;
+    if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+    if constexpr (EPI == EPI_RESID) s_h2[idx] = h2;
+    if constexpr (EPI == EPI_ARGMAX)
+      s_best[idx] = make_float2(ok ? round_bf16(tot) : -INFINITY,
+                                __int_as_float(ok ? n : 0x7fffffff));
+  }
+  if constexpr (EPI == EPI_RESID) {
+    if (a.ss_out) {
+      __syncthreads();
+      if (t < M && t < mr) {
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sum += s_h2[t * R + r];
+        atomicAdd(a.ss_out + t, sum);
+      }
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    __syncthreads();
+    if (t < M && t < mr) {
+      float2 best = s_best[t * R];
+      for (int r = 1; r < R; ++r) {
+        const float2 c = s_best[t * R + r];
+        if (c.x > best.x) best = c;  // columns ascend with r: ties keep the lower index
+      }
+      a.part[(long long)t * a.nparts + blockIdx.x] = best;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // layout 1: one wavefront per RW output columns, WPB wavefronts per workgroup
 // ---------------------------------------------------------------------------
@@ -657,8 +792,30 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
   }
 }
 
+template <int M, int R, int CPT>
+int launch_row(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  const dim3 grid((a.N + R - 1) / R), block(NT);
+#define KO_G(NORMV, EPIV) \
+  hipLaunchKernelGGL((gemv_row_kernel<M, R, NORMV, EPIV, CPT>), grid, block, 0, s, a)
+  switch (epi) {
+    case EPI_F32: if (norm) KO_G(true, EPI_F32); else KO_G(false, EPI_F32); break;
+    case EPI_BF16: if (norm) KO_G(true, EPI_BF16); else KO_G(false, EPI_BF16); break;
+    case EPI_RESID: if (norm) KO_G(true, EPI_RESID); else KO_G(false, EPI_RESID); break;
+    case EPI_SWIGLU: if (norm) KO_G(true, EPI_SWIGLU); else KO_G(false, EPI_SWIGLU); break;
+    default: if (norm) KO_G(true, EPI_ARGMAX); else KO_G(false, EPI_ARGMAX); break;
+  }
+#undef KO_G
+  return KO_LAUNCH_STATUS();
+}
+
 template <int M, int R>
 int launch_block(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
+  // 1-2 rows with K <= 10240: the register-resident row kernel
+  if constexpr (M <= 2 && R <= 8) {
+    const int KC = a.K >> 3;
+    if (KC <= 2 * NT) return launch_row<M, R, 2>(a, epi, norm, s);
+    if (KC <= 5 * NT && !(epi == EPI_SWIGLU && R > 4)) return launch_row<M, R, 5>(a, epi, norm, s);
+  }
   const dim3 grid((a.N + R - 1) / R), block(NT);
 #define KO_G(NORMV, EPIV) \
   hipLaunchKernelGGL((gemv_block_kernel<M, R, NORMV, EPIV>), grid, block, 0, s, a)
