@@ -31,9 +31,10 @@ extern "C" {
  * unit     keys per work unit (multiple of 16); max_units*unit >= cap. Each unit
  *          leaves one fp32 partial slot per query row.
  * grid_waves  number of wavefronts launched (they stride over the units). With
- *          T == 1 (and no counters) a unit is split over the wavefronts of one
- *          workgroup: 4 when unit % 64 == 0, else 2 when unit % 32 == 0, else 1,
- *          so grid_waves should be a multiple of that count.
+ *          T == 1 a unit is split over the wavefronts of one workgroup: 8 when
+ *          unit >= 1024 and unit % 128 == 0, else 4 when unit % 64 == 0, else 2
+ *          when unit % 32 == 0, else 1, so grid_waves should be a multiple of
+ *          that count.
  * o_part   [B*T*nq*max_units*head_dim] fp32 scratch, ml [B*T*nq*max_units*2] fp32.
  * T in 1..4, head_dim 128. */
 int ko_decode_attn_partial(const void* q, const void* k_cache, const void* v_cache,
@@ -53,8 +54,10 @@ int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_l
  * ko_decode_attn_partial followed by ko_decode_attn_combine, the reference's
  * two launches. With counters ([B*nkv] int32, zero before the first call;
  * every call leaves them zero) it is one launch: the last work unit of each
- * (sequence, KV head) merges that pair's partials after a device-scope fence
- * per unit. */
+ * (sequence, KV head) merges that pair's partials. For T == 1 the partials and
+ * the arrival count travel through device-coherent (agent-scope) stores, loads
+ * and atomics; for T > 1 each unit publishes its partials with a device-scope
+ * fence. */
 int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens,
                    int len_offset, int cap, long long cache_b_stride, long long cache_h_stride,
                    int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,

@@ -676,15 +676,17 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
     bf16x8 qa[4];
     uint4 knew[4], vnew;
     if constexpr (QKV) {
-      constexpr int NH = G / WM;  // q heads normed by each wavefront
+      // q heads normed by each wavefront (wavefronts past the 4th norm none)
+      constexpr int NH = G / WM > 0 ? G / WM : 1;
+      const bool has_q = wave < G;
       const int nqkv = (nq + 2 * nkv) * D;
       const int pt = min(max(pnew, 0), a.max_pos - 1);
       const uint16_t* src = a.qkv + (long long)b * nqkv;
-      const bool do_k = new_unit && wave == 0;
+      const bool do_k = new_unit && wave == (WM > G ? G : 0);  // the new key: an idle wavefront if any
       uint32_t xh[NH], xk = 0, kwv = 0, vv = 0;
 #pragma unroll
       for (int n = 0; n < NH; ++n)
-        xh[n] = reinterpret_cast<const uint32_t*>(src + (kvh * G + wave + n * WM) * D)[lane];
+        xh[n] = has_q ? reinterpret_cast<const uint32_t*>(src + (kvh * G + wave + n * WM) * D)[lane] : 0u;
       const uint32_t qwv = reinterpret_cast<const uint32_t*>(a.qw)[lane];
       const uint32_t cwv = reinterpret_cast<const uint32_t*>(a.cosb + (long long)pt * D)[lane];
       const uint32_t swv = reinterpret_cast<const uint32_t*>(a.sinb + (long long)pt * D)[lane];
@@ -695,8 +697,10 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
       }
       if (has_new) vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
       asm volatile("" ::: "memory");  // keep every load above ahead of the first wait
+      if (has_q) {
 #pragma unroll
-      for (int n = 0; n < NH; ++n) lds_q[wave + n * WM][lane] = norm_rope2(xh[n], qwv, cwv, swv, a.eps);
+        for (int n = 0; n < NH; ++n) lds_q[wave + n * WM][lane] = norm_rope2(xh[n], qwv, cwv, swv, a.eps);
+      }
       if (do_k) {
         // the new key: to LDS for the wavefront that owns it, and the KV
         // append at slot pnew (fused.py:88-96)
@@ -877,13 +881,21 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
       const long long R = (long long)b * nq + kvh * G + j;
       float* dst = a.o_part + (R * max_units + c) * D + d0;
       if constexpr (FUSED) {
+        if constexpr (V == 1) {
+          __hip_atomic_store(dst, o[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
 #pragma unroll
-        for (int v = 0; v < V; v += 2) store_coherent(dst + v, make_float2(o[v], o[v + 1]));
+          for (int v = 0; v < V; v += 2) store_coherent(dst + v, make_float2(o[v], o[v + 1]));
+        }
         if (d0 == 0) store_coherent(a.ml + 2 * (R * max_units + c), make_float2(Mx, L));
       } else {
+        if constexpr (V == 1) {
+          dst[0] = o[0];
+        } else {
 #pragma unroll
-        for (int v = 0; v < V; v += 2)
-          reinterpret_cast<float2*>(dst + v)[0] = make_float2(o[v], o[v + 1]);
+          for (int v = 0; v < V; v += 2)
+            reinterpret_cast<float2*>(dst + v)[0] = make_float2(o[v], o[v + 1]);
+        }
         if (d0 == 0) reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(Mx, L);
       }
     }
@@ -946,9 +958,13 @@ int launch(const AttnArgs& a, int grid_waves, hipStream_t s) {
   return KO_LAUNCH_STATUS();
 }
 
-// Wavefronts per workgroup of attn1_kernel for a unit size: the largest of
-// 4, 2, 1 that splits the unit into whole 16-key steps.
-int waves_per_unit(int unit) { return unit % 64 == 0 ? 4 : unit % 32 == 0 ? 2 : 1; }
+// Wavefronts per workgroup of attn1_kernel for a unit size: 8 for long units
+// (>= 1024 keys, at least 8 steps per wavefront), else the largest of 4, 2, 1
+// that splits the unit into whole 16-key steps.
+int waves_per_unit(int unit) {
+  if (unit >= 1024 && unit % 128 == 0) return 8;
+  return unit % 64 == 0 ? 4 : unit % 32 == 0 ? 2 : 1;
+}
 
 template <bool QKV, int WM, bool FUSED>
 int launch1_wm(const AttnArgs& a, int grid_waves, hipStream_t s) {
@@ -960,6 +976,7 @@ int launch1_wm(const AttnArgs& a, int grid_waves, hipStream_t s) {
 template <bool QKV, bool FUSED>
 int launch1(const AttnArgs& a, int grid_waves, hipStream_t s) {
   switch (waves_per_unit(a.unit)) {
+    case 8: return launch1_wm<QKV, 8, FUSED>(a, grid_waves, s);
     case 4: return launch1_wm<QKV, 4, FUSED>(a, grid_waves, s);
     case 2: return launch1_wm<QKV, 2, FUSED>(a, grid_waves, s);
     default: return launch1_wm<QKV, 1, FUSED>(a, grid_waves, s);

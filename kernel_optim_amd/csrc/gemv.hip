@@ -734,8 +734,7 @@ __global__ __launch_bounds__(256) void gemv_tile_kernel(const uint16_t* __restri
 }
 
 // One 1024-thread workgroup per row m: argmax over the work units' (value,
-// index) pairs with the lowest index on ties, loads issued 8 per thread at a
-// time. Optionally pos[m] += 1 (the decode step's position advance,
+// index) pairs with the lowest index on ties. Optionally pos[m] += 1 (the decode step's position advance,
 // engine.py:292) and h[m] = emb[ids[m]] (the next step's embedding gather,
 // gemv.py:201-211, so the next step needs no gather launch).
 constexpr int FT = 1024;
@@ -745,6 +744,32 @@ __device__ __forceinline__ void better(float v, int i, float& bv, int& bi) {
     bi = i;
   }
 }
+__device__ __forceinline__ void better_xor16(float& v, int& i) {
+  const unsigned vb = __builtin_bit_cast(unsigned, v);
+  const auto pv = __builtin_amdgcn_permlane16_swap(vb, vb, false, false);
+  const auto pi = __builtin_amdgcn_permlane16_swap((unsigned)i, (unsigned)i, false, false);
+  // rows {0,0,2,2} and {1,1,3,3}: take the better of the two in every lane
+  float a = __builtin_bit_cast(float, (unsigned)pv[0]), b = __builtin_bit_cast(float, (unsigned)pv[1]);
+  int ia = (int)pi[0], ib = (int)pi[1];
+  better(b, ib, a, ia);
+  v = a;
+  i = ia;
+}
+__device__ __forceinline__ void better_xor32(float& v, int& i) {
+  const unsigned vb = __builtin_bit_cast(unsigned, v);
+  const auto pv = __builtin_amdgcn_permlane32_swap(vb, vb, false, false);
+  const auto pi = __builtin_amdgcn_permlane32_swap((unsigned)i, (unsigned)i, false, false);
+  float a = __builtin_bit_cast(float, (unsigned)pv[0]), b = __builtin_bit_cast(float, (unsigned)pv[1]);
+  int ia = (int)pi[0], ib = (int)pi[1];
+  better(b, ib, a, ia);
+  v = a;
+  i = ia;
+}
+
+// All of a row's partial loads are issued before the first comparison (up to
+// FL per thread, 24 x 1024 = 24576 work units in one round); the wave-level
+// reductions use DPP and the gfx950 permlane swaps.
+constexpr int FL = 24;
 __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
     const float2* __restrict__ part, int nparts, long long* __restrict__ ids,
     int* __restrict__ pos, const uint16_t* __restrict__ emb, uint16_t* __restrict__ h, int H,
@@ -755,22 +780,30 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
   const float2* pr = part + (long long)m * nparts;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i0 = t; i0 < nparts; i0 += 8 * FT) {
-    float2 c[8];
+  for (int i0 = t; i0 < nparts; i0 += FL * FT) {
+    float2 c[FL];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < FL; ++j) {
       const int i = i0 + j * FT;
       c[j] = i < nparts ? pr[i] : make_float2(-INFINITY, __int_as_float(0x7fffffff));
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) better(c[j].x, __float_as_int(c[j].y), bv, bi);
+    for (int j = 0; j < FL; ++j) better(c[j].x, __float_as_int(c[j].y), bv, bi);
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const int oi = __shfl_xor(bi, off, 64);
-    better(ov, oi, bv, bi);
+  // within 16-lane rows (DPP row_ror), then across rows
+#define KO_FIN_STEP(CTRL)                                                                   \
+  {                                                                                         \
+    const float ov = dpp_f<CTRL>(bv);                                                       \
+    const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xf, 0xf, false);               \
+    better(ov, oi, bv, bi);                                                                 \
   }
+  KO_FIN_STEP(0x128)
+  KO_FIN_STEP(0x124)
+  KO_FIN_STEP(0x122)
+  KO_FIN_STEP(0x121)
+#undef KO_FIN_STEP
+  better_xor16(bv, bi);
+  better_xor32(bv, bi);
   if (lane == 0) s_best[wv] = make_float2(bv, __int_as_float(bi));
   __syncthreads();
   if (t == 0) {
