@@ -80,6 +80,32 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
                        int max_units, int grid_waves, float eps, float scale, float* o_part,
                        float* ml, int* counters, void* out, void* stream);
 
+/* ko_decode_attn_qkv (with counters) and the o projection with its residual add
+ * in ONE launch, for B <= 2 and unit % 64 == 0, unit < 1024 (4 wavefronts per
+ * unit): out [B, nq*head_dim] receives the merged attention output as before,
+ * and h [B, H] <- bf16(h + bf16(out @ w_o^T)) (w_o [H, nq*head_dim] bf16), the
+ * RESID GEMV of engine/engine.py:330-331 (kernels/gemv.py EPI_RESID). Extra
+ * workgroups own 8 columns of the projection each; they load their weights while
+ * the attention runs and wait on a device-coherent count of merged (sequence,
+ * KV head) pairs. sync: ko_decode_attn_qkv_oproj_sync_ints() int32 (zero before
+ * the first call; every call leaves it zero); err [1] int32 is set to 1 if that
+ * wait ever gave up (never expected; the results of such a call are invalid).
+ * delay_ns: how long the projection workgroups hold their weight loads so the
+ * attention's first loads go ahead of them (0: no delay). Replaces
+ * engine.py:328-332 (attention, o projection and its residual add); no single
+ * reference function. */
+int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, const void* cos,
+                             const void* sin, int max_pos, const int* pos, void* k_cache,
+                             void* v_cache, int cap, long long cache_b_stride,
+                             long long cache_h_stride, int B, int nkv, int head_dim, int unit,
+                             int max_units, int grid_waves, float eps, float scale,
+                             float* o_part, float* ml, int* counters, void* out,
+                             const void* w_o, void* h, int H, int* sync, int* err,
+                             int delay_ns, void* stream);
+
+/* int32 elements of ko_decode_attn_qkv_oproj's sync array (a size, not a status). */
+long long ko_decode_attn_qkv_oproj_sync_ints(void);
+
 /* ---- residual add + RMSNorm ---------------------------------------------
  * Replaces engine/kernels/fused.py:16-36 (_add_rms_norm_kernel) as launched by
  * add_rms_norm (fused.py:39-46). res [rows, n] bf16 (updated in place to

@@ -36,7 +36,7 @@
 //           next launch.
 #include <type_traits>
 
-#include "ko_common.h"
+#include "gemv_core.h"
 
 using namespace ko;
 
@@ -47,6 +47,14 @@ constexpr int G = 4;            // query heads per KV head
 constexpr int WAVES = 4;        // wavefronts per workgroup
 constexpr float TAU = 8.0f;     // lazy-rescale threshold, log2 units
 constexpr float NEG_BIG = -1.0e30f;
+
+constexpr int SPIN_MAX = 1 << 21;
+// sync[] layout of ko_decode_attn_qkv_oproj: [0] merged-pair count, [1] projection
+// workgroups past their wait, then OPROJ_FLAGS done-flag copies 128 bytes apart.
+// Each flag line also carries, one int further on, the count of projection
+// workgroups of that flag's group that have finished (re-arm bookkeeping).
+constexpr int OPROJ_FLAG0 = 32, OPROJ_FLAG_STRIDE = 32, OPROJ_FLAGS = 32;
+constexpr int OPROJ_SYNC_INTS = OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * OPROJ_FLAGS;
 
 struct AttnArgs {
   const uint16_t* q;     // [B*T, nq*D] (unless QKV)
@@ -68,6 +76,7 @@ struct AttnArgs {
   float* ml;
   int* counters;         // [B*nkv] (FUSED)
   uint16_t* out;         // [B*T, nq*D] (FUSED)
+  int* pairs_done;       // attention + o projection launch: merged (b, kv_head) pairs
 };
 
 __device__ __forceinline__ int nunits(int len, int unit) {
@@ -196,7 +205,7 @@ __device__ __forceinline__ void store_coherent(float* p, float2 v) {
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NB, bool COHERENT = false>
+template <int NB, bool COHERENT = false, bool COH_OUT = false>
 __device__ void combine_row(const float* __restrict__ o_part, const float* __restrict__ ml,
                             long long R, int n, const int* len_ptr, int len_off, int cap,
                             int unit, int max_units, uint16_t* __restrict__ out) {
@@ -237,7 +246,11 @@ __device__ void combine_row(const float* __restrict__ o_part, const float* __res
   }
   const float r0 = L > 0.f ? o0 / L : 0.f;
   const float r1 = L > 0.f ? o1 / L : 0.f;
-  reinterpret_cast<uint32_t*>(out + R * D)[lane] = pack_bf16x2(r0, r1);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out + R * D) + lane;
+  if constexpr (COH_OUT)  // read later in the same launch: a device-coherent store
+    __hip_atomic_store(dst, pack_bf16x2(r0, r1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *dst = pack_bf16x2(r0, r1);
 }
 
 template <int T, bool QKV, bool FUSED>
@@ -593,8 +606,12 @@ __device__ __forceinline__ uint32_t norm_rope2(uint32_t x, uint32_t w, uint32_t 
 //     the QK^T result holds the same 16 scores (the A rows are the 4 heads
 //     replicated), so the running max stays wave-uniform without cross-row
 //     traffic.
-template <bool QKV, int WM, bool FUSED>
-__global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
+// wg / nwg: this workgroup's index among the nwg attention workgroups.
+// OPROJ (with FUSED): the merged outputs are stored device-coherently and each
+// merge bumps a.pairs_done, for the o-projection workgroups of the same launch.
+template <bool QKV, int WM, bool FUSED, bool OPROJ = false>
+__device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg) {
+  static_assert(!OPROJ || FUSED, "the o projection consumes the merged output");
   __shared__ int lds_prev;
   __shared__ __align__(16) uint16_t lds_p[WM][G * 16];
   __shared__ __align__(16) float lds_acc[WM][4][G][D];  // [wave][key group g][head][col]
@@ -620,7 +637,7 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
     total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
   }
 
-  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+  for (int u = wg; u < total; u += nwg) {
     const int pidx = u / nkv;
     const int kvh = u - pidx * nkv;
     int b, c, kv_len;
@@ -913,12 +930,100 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
       const int n = nunits(kv_len, unit);
       if (lds_prev == n - 1) {
         for (int j = wave; j < G; j += WM)
-          combine_row<32, true>(a.o_part, a.ml, (long long)b * nq + kvh * G + j, n, nullptr, 0,
-                                a.cap, unit, max_units, a.out);
-        if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          combine_row<32, true, OPROJ>(a.o_part, a.ml, (long long)b * nq + kvh * G + j, n,
+                                       nullptr, 0, a.cap, unit, max_units, a.out);
+        if constexpr (OPROJ) {
+          __builtin_amdgcn_s_waitcnt(0);  // this wave's merged row is performed
+          __syncthreads();
+        }
+        [[maybe_unused]] const int live_pairs = __popcll(__ballot(my_n > 0)) * nkv;
+        if (threadIdx.x == 0) {
+          __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if constexpr (OPROJ) {
+            // the pair that completes the count raises the done flag (one copy
+            // per 128-byte line, so its waiters do not queue on one address)
+            const int live = live_pairs;
+            const int prev =
+                __hip_atomic_fetch_add(a.pairs_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == live - 1) {
+              for (int f = 0; f < OPROJ_FLAGS; ++f)
+                __hip_atomic_store(a.pairs_done + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * f, 1,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+        }
       }
     }
     __syncthreads();  // the next unit reuses the LDS
+  }
+}
+
+template <bool QKV, int WM, bool FUSED>
+__global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
+  attn1_body<QKV, WM, FUSED>(a, blockIdx.x, gridDim.x);
+}
+
+// Decode attention and the o projection in one launch (one query token, 1-2
+// sequences, 4 wavefronts per unit). Workgroups [0, nattn) run the attention
+// units with the fused combine; the rest each own 8 output columns of the o
+// projection: they issue all their weight loads, wait until every (b, kv_head)
+// pair has been merged (a device-coherent counter), then read the merged
+// attention output with device-scope loads and finish as the RESID GEMV
+// (h <- bf16(h + bf16(W_o attn))). The o-projection weights thus stream while
+// the attention's latency chain runs instead of after it. Workgroups are
+// dispatched in index order, so every attention workgroup is resident before
+// any o-projection workgroup waits; the wait is also bounded (SPIN_MAX polls,
+// then *err is set and the workgroup goes on). The last o-projection workgroup
+// through the wait re-arms both counters for the next launch.
+
+
+template <bool QKV, int M>
+__global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g, int nattn,
+                                                         int delay_ticks, int* err) {
+  if ((int)blockIdx.x < nattn) {
+    attn1_body<QKV, 4, true, true>(a, blockIdx.x, nattn);
+    return;
+  }
+  const int wg = blockIdx.x - nattn;
+  const int nog = gridDim.x - nattn;
+  // Let the attention's first (latency-critical) loads go ahead of this
+  // workgroup's weight stream: a short wait on the real-time counter.
+  if (delay_ticks > 0) {
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < (unsigned long long)delay_ticks) __builtin_amdgcn_s_sleep(4);
+  }
+  const int grp = wg % OPROJ_FLAGS;
+  int* flag = a.pairs_done + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * grp;
+  auto wait_x = [&] {
+    if (threadIdx.x == 0) {
+      int it = 0;
+      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        __builtin_amdgcn_s_sleep(8);
+        if (++it >= SPIN_MAX) {
+          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+  };
+  gemv_row_body<M, 8, false, EPI_RESID, 2, true>(g, wg, wait_x);
+  // Re-arm for the next launch, off the critical path: the last workgroup of a
+  // flag group clears that flag and counts the group; the last group clears the
+  // pair count and the group count.
+  if (threadIdx.x == 0) {
+    const int in_grp = (nog - grp + OPROJ_FLAGS - 1) / OPROJ_FLAGS;  // workgroups of group grp
+    if (__hip_atomic_fetch_add(flag + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        in_grp - 1) {
+      __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(flag + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int groups = nog < OPROJ_FLAGS ? nog : OPROJ_FLAGS;
+      if (__hip_atomic_fetch_add(a.pairs_done + 1, 1, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == groups - 1) {
+        __hip_atomic_store(a.pairs_done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.pairs_done + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 
@@ -1105,6 +1210,59 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
   if (st) return st;
   return ko_decode_attn_combine(o_part, ml, pos, 1, cap, B, 1, nkv * G, head_dim, unit,
                                 max_units, out, stream);
+}
+
+long long ko_decode_attn_qkv_oproj_sync_ints(void) { return OPROJ_SYNC_INTS; }
+
+int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, const void* cos,
+                             const void* sin, int max_pos, const int* pos, void* k_cache,
+                             void* v_cache, int cap, long long cache_b_stride,
+                             long long cache_h_stride, int B, int nkv, int head_dim, int unit,
+                             int max_units, int grid_waves, float eps, float scale,
+                             float* o_part, float* ml, int* counters, void* out,
+                             const void* w_o, void* h, int H, int* sync, int* err,
+                             int delay_ns, void* stream) {
+  int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
+                        head_dim, unit, max_units, o_part, ml);
+  if (st) return st;
+  if (!qkv || !q_w || !k_w || !cos || !sin || !out || !counters || !w_o || !h || !sync || !err ||
+      max_pos < 1 || grid_waves < 4 || H < 8 || (H & 7))
+    return KO_EINVAL;
+  if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
+      !aligned16(sin) || !aligned16(out) || !aligned16(w_o) || !aligned16(h))
+    return KO_EINVAL;
+  if (B > 2 || waves_per_unit(unit) != 4) return KO_ENOTSUP;
+  const int K = nkv * G * D;  // o projection input width
+  if (K > 2 * GEMV_NT * 8) return KO_ENOTSUP;
+  AttnArgs a = base_args(k_cache, v_cache, pos, 1, cap, cache_b_stride, cache_h_stride, B, nkv,
+                         unit, max_units, scale, o_part, ml);
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.qw = static_cast<const uint16_t*>(q_w);
+  a.kw = static_cast<const uint16_t*>(k_w);
+  a.cosb = static_cast<const uint16_t*>(cos);
+  a.sinb = static_cast<const uint16_t*>(sin);
+  a.eps = eps;
+  a.max_pos = max_pos;
+  a.counters = counters;
+  a.out = static_cast<uint16_t*>(out);
+  a.pairs_done = sync;
+  GemvArgs g = {};
+  g.x = static_cast<const uint16_t*>(out);
+  g.w = static_cast<const uint16_t*>(w_o);
+  g.h = static_cast<uint16_t*>(h);
+  g.mrows = B;
+  g.N = H;
+  g.K = K;
+  g.eps = eps;
+  const int nattn = grid_waves / 4;
+  const dim3 grid(nattn + (H + 7) / 8), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int ticks = delay_ns > 0 ? delay_ns / 10 : 0;  // s_memrealtime runs at 100 MHz
+  if (B == 1)
+    hipLaunchKernelGGL((attn_oproj_kernel<true, 1>), grid, block, 0, s, a, g, nattn, ticks, err);
+  else
+    hipLaunchKernelGGL((attn_oproj_kernel<true, 2>), grid, block, 0, s, a, g, nattn, ticks, err);
+  return KO_LAUNCH_STATUS();
 }
 
 }  // extern "C"

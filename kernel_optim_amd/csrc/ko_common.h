@@ -60,6 +60,16 @@ __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
   return r;
 }
 
+// 16-byte load at device (agent) scope: two relaxed agent-scope 8-byte atomic
+// loads (global_load ... sc1), for data that other workgroups of the same
+// launch wrote with agent-scope stores.
+__device__ __forceinline__ uint4 ldg16_coherent(const void* p) {
+  unsigned long long* q = reinterpret_cast<unsigned long long*>(const_cast<void*>(p));
+  const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 // ---- cross-lane reductions -------------------------------------------------

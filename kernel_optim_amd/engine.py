@@ -41,6 +41,9 @@ DEVICE = "cuda:0"
 LOG = os.environ.get("ENGINE_LOG", "0") == "1"
 TUNE = os.environ.get("ENGINE_TUNE", "1") == "1"
 TUNE_BUDGET_S = 60.0
+# attention and the o projection in one launch for 1-2 sequences (ENGINE_FUSE_OPROJ=0: two)
+FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
+OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
 
 
 def _rope_tables(n, d, theta, device):
@@ -127,6 +130,7 @@ class Engine:
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
+        self.attn.oproj_delay_ns = OPROJ_DELAY_NS
         H, L = cfg.hidden, self.w["layers"]
         e = cfg.eps
         self.gv = dict(
@@ -164,12 +168,18 @@ class Engine:
         cfg = self.cfg
         g, W = self.gv, self.gw  # W: each projection's weights in its launch layout
         h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
+        fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
         for i, lw in enumerate(self.w["layers"]):
             g["qkv"](h, W["qkv"][i], y=self.qkv, nw=lw["w_in"])
-            self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
-                                 self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
-                                 cfg.eps)
-            g["o"](self.attn_out, W["o"][i], h=h)
+            if fuse_o:  # attention + o projection + residual in one launch
+                self.attn.decode_qkv_oproj(self.qkv, lw["q_norm"], lw["k_norm"], self._cos,
+                                           self._sin, self.pos, self.k_cache[i], self.v_cache[i],
+                                           self.attn_out, cfg.eps, lw["o"], h)
+            else:
+                self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
+                                     self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
+                                     cfg.eps)
+                g["o"](self.attn_out, W["o"][i], h=h)
             g["gu"](h, W["gu"][i], y=self.act, nw=lw["w_post"])
             g["down"](self.act, W["down"][i], h=h)
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,

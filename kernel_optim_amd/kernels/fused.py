@@ -102,6 +102,11 @@ class DecodeAttention:
         # per-(sequence, KV head) arrival counters; every launch leaves them at zero
         self.counters = (torch.zeros(B * nkv, dtype=torch.int32, device=device) if fused_combine
                          else None)
+        # decode_qkv_oproj: its counters and done flags, and its wait-failure flag
+        self.sync = torch.zeros(_lib.lib().ko_decode_attn_qkv_oproj_sync_ints(), dtype=torch.int32,
+                                device=device)
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        self.oproj_delay_ns = 1000
         self.scale = d ** -0.5
 
     def _check_kv(self, k_cache, v_cache, lens):
@@ -131,6 +136,41 @@ class DecodeAttention:
         """Ragged form: lengths[b] = number of valid keys of sequence b (int32);
         the T queries sit at positions lengths[b]-T .. lengths[b]-1."""
         self._run(q, k_cache, v_cache, lengths, 0, out)
+
+    def oproj_fusable(self):
+        """decode_qkv_oproj serves 1-2 sequences with the fused combine and 4
+        wavefronts per unit (attention.hip, ko_decode_attn_qkv_oproj)."""
+        return (self.B <= 2 and self.counters is not None and self.waves_per_unit == 4
+                and self.nq * self.d <= 4096)
+
+    def decode_qkv_oproj(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, w_o, h):
+        """decode_qkv and then the o projection with its residual add, in one launch:
+        out as decode_qkv leaves it, and h <- bf16(h + bf16(out @ w_o^T)) (the RESID
+        GEMV of engine.py:330-331). The projection's weights stream while the
+        attention runs. w_o: [H, nq*d] bf16; h: [B, H] bf16."""
+        B, nq, nkv, d = self.B, self.nq, self.nkv, self.d
+        _need(self.oproj_fusable(), "decode_qkv_oproj needs B <= 2, fused_combine and a unit "
+                                    "of 4 wavefronts")
+        _check(qkv, "qkv", BF16, (B, (nq + 2 * nkv) * d))
+        _check(out, "out", BF16, (B, nq * d))
+        _check(q_w, "q_w", BF16, (d,))
+        _check(k_w, "k_w", BF16, (d,))
+        _check(cos, "cos", BF16)
+        _check(sin, "sin", BF16)
+        _need(cos.dim() == 2 and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape),
+              "cos/sin must be [rows, d]")
+        _need(h.dim() == 2 and h.shape[0] == B, "h must be [B, H]")
+        H = h.shape[1]
+        _check(h, "h", BF16, (B, H))
+        _check(w_o, "w_o", BF16, (H, nq * d))
+        self._check_kv(k_cache, v_cache, pos)
+        _lib.call("ko_decode_attn_qkv_oproj", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w),
+                  _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], _lib.ptr(pos), _lib.ptr(k_cache),
+                  _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
+                  self.unit, self.max_units, self.grid_waves, eps, self.scale,
+                  _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters), _lib.ptr(out),
+                  _lib.ptr(w_o), _lib.ptr(h), H, _lib.ptr(self.sync), _lib.ptr(self.err),
+                  self.oproj_delay_ns, _lib.stream_ptr())
 
     def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps):
         """Decode step (T=1) straight from the bf16 QKV projection [B, (nq+2nkv)*d]:

@@ -237,3 +237,60 @@ def test_decode_qkv_matches_norm_rope_append_then_attention(dev, B, cap, unit, f
     from tests.bf16util import assert_bf16_close
     assert_bf16_close(k.cpu(), kref, max_frac=1e-3)
     assert torch.equal(v.cpu(), vref)
+
+
+@pytest.mark.parametrize("B,cap,pos0", [(1, 1296, 1024), (1, 1296, 0), (2, 640, 517)])
+def test_decode_qkv_oproj_equals_attention_then_o_gemv(dev, B, cap, pos0):
+    """The one-launch attention + o projection equals decode_qkv followed by the RESID
+    GEMV (engine.py:328-331) bit for bit -- same merged attention rows, same
+    dot-product order -- including the KV append, over several graph replays whose
+    positions advance (the launch re-arms its counters every time)."""
+    from oracle import ops as O
+    from kernel_optim_amd.kernels import gemv as GV
+    fused_mod = _fused()
+    nq, nkv, d, H = 32, 8, 128, 2560
+    g = torch.Generator(device=dev).manual_seed(60 + B)
+    qkv = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
+    k0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    v0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    w_o = (0.02 * torch.randn(H, nq * d, device=dev, generator=g)).to(torch.bfloat16)
+    h0 = torch.randn(B, H, device=dev, generator=g).to(torch.bfloat16)
+    pos_start = torch.tensor([pos0, max(pos0 - 300, 0)][:B], dtype=torch.int32, device=dev)
+
+    def run(fused_launch, steps):
+        k, v, h = k0.clone(), v0.clone(), h0.clone()
+        pos = pos_start.clone()
+        att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, fused_combine=True)
+        o = GV.Gemv(B, H, nq * d, GV.EPI_RESID, norm=False)
+        out = torch.zeros(B, nq * d, device=dev, dtype=torch.bfloat16)
+
+        def step():
+            if fused_launch:
+                att.decode_qkv_oproj(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6, w_o, h)
+            else:
+                att.decode_qkv(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6)
+                o(out, w_o, h=h, cfg=(0, 8, 0))
+            pos.add_(1)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(steps - 1):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.all(att.counters == 0) and torch.all(att.sync == 0)
+        assert int(att.err.item()) == 0, "the o projection's wait gave up"
+        return out.cpu(), h.cpu(), k.cpu(), v.cpu()
+
+    want = run(False, 4)
+    got = run(True, 4)
+    for name, a, b in zip(("out", "h", "k", "v"), got, want):
+        assert torch.equal(a, b), name
