@@ -106,43 +106,6 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
 /* int32 elements of ko_decode_attn_qkv_oproj's sync array (a size, not a status). */
 long long ko_decode_attn_qkv_oproj_sync_ints(void);
 
-/* ---- every decoder layer of one decode step, one launch ------------------
- * Replaces the per-layer loop of engine/engine.py:325-335 for one query token
- * per sequence (add_rms_norm, qkv projection, qk_norm_rope, decode attention,
- * o projection + residual, add_rms_norm, gate|up projection, silu_mul, down
- * projection + residual), with the arithmetic of the separate entry points:
- * ko_gemv layout 0 with 8 output columns per workgroup and
- * ko_decode_attn_qkv with the fused combine. B <= 2, head_dim 128, nq = 4*nkv,
- * a unit the attention splits over 4 wavefronts (unit % 64 == 0, and unit
- * < 1024 or unit % 128 != 0), H and I multiples of 8, H <= 4096,
- * nq*128 <= 4096, I <= 10240.
- * layer_table: device array [L][10] of pointers per layer: w_in [H],
- *   qkv [(nq+2nkv)*128, H], q_norm [128], k_norm [128], o [H, nq*128],
- *   w_post [H], gu [2I, H] (gate rows then up rows), down [H, I], and the
- *   layer's k_cache and v_cache [B, nkv, cap, 128] (strides cache_b_stride,
- *   cache_h_stride, shared by all layers).
- * h [B, H]: in, the step's input embeddings; out, the last layer's residual
- * stream. qkv [B, (nq+2nkv)*128], attn [B, nq*128], act [B, I]: scratch.
- * pos [B]: the new token's position (its KV slot; keys 0..pos are attended).
- * o_part / ml as for ko_decode_attn_qkv; counters [L*B*nkv] and sync
- * [ko_decode_layers_sync_ints(L)] int32 zero before the first call (every
- * call leaves them zero); err [1] set to 1 if a stage wait gave up (never
- * expected; the results of such a call are invalid). gemv_wgs: host array of
- * 4 workgroup counts for the qkv, o, gate|up and down stages (each workgroup
- * takes every n-th group of 8, 8, 4, 4 output columns; an entry <= 0, or NULL,
- * picks the default; a count that leaves a workgroup fewer than 2 or more than
- * 32 groups is an error). delay_ns: how long the o-projection workgroups hold
- * their weight loads behind the attention's. */
-int ko_decode_layers(const void* layer_table, int L, void* h, void* qkv, void* attn, void* act,
-                     int B, int H, int I, int nkv, int head_dim, const void* cos, const void* sin,
-                     int max_pos, const int* pos, int cap, long long cache_b_stride,
-                     long long cache_h_stride, int unit, int max_units, int grid_waves, float eps,
-                     float scale, float* o_part, float* ml, int* counters, int* sync, int* err,
-                     const int* gemv_wgs, int delay_ns, void* stream);
-
-/* int32 elements of ko_decode_layers' sync array for L layers (a size). */
-long long ko_decode_layers_sync_ints(int L);
-
 /* ---- residual add + RMSNorm ---------------------------------------------
  * Replaces engine/kernels/fused.py:16-36 (_add_rms_norm_kernel) as launched by
  * add_rms_norm (fused.py:39-46). res [rows, n] bf16 (updated in place to

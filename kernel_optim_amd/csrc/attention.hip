@@ -430,9 +430,7 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
 // The pair that completes the count of live pairs raises the done flag (one
 // copy per 128-byte line, so its waiters do not queue on one address).
 struct OprojHooks {
-  static constexpr bool kWaitInput = false;
   static constexpr bool kNotify = true;
-  __device__ void wait_input() const {}
   __device__ void merged(const AttnArgs& a, int live) const {
     const int prev =
         __hip_atomic_fetch_add(a.pairs_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

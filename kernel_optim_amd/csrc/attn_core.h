@@ -1,7 +1,7 @@
 // One-query-token split-K GQA decode attention body for gfx950, shared by the
-// attention launches (attention.hip) and the whole-step decode launch
-// (decode_layers.hip): argument block, unit enumeration over ragged lengths,
-// the log-sum-exp combine, and the per-workgroup unit loop. Semantics are those
+// attention launches of attention.hip (alone, and with the o projection in the
+// same launch): argument block, unit enumeration over ragged lengths, the
+// log-sum-exp combine, and the per-workgroup unit loop. Semantics are those
 // of engine/kernels/fused.py:138-234 with the per-head q/k RMSNorm + RoPE and
 // KV append of fused.py:54-96 folded in (QKV).
 #pragma once
@@ -209,19 +209,14 @@ __device__ __forceinline__ uint32_t norm_rope2(uint32_t x, uint32_t w, uint32_t 
 //     traffic.
 // wg / nwg: this workgroup's index among the nwg attention workgroups.
 //
-// Hooks: what a launch that holds the producer of qkv or the consumer of the
-// merged output adds (NoAttnHooks: nothing).
-//   kWaitInput: qkv is written earlier in the same launch: wait_input() (all
-//     threads of the workgroup) runs once, after the first unit's K/V loads are
-//     issued and before qkv is read, and qkv is read with device-scope loads.
-//   kNotify (with FUSED): the merged output is read later in the same launch:
-//     it is stored device-coherently, and once a pair's merged rows are
-//     performed thread 0 calls merged(a, live_pairs). no_units() runs on
-//     workgroup 0 when no sequence has a key (then nothing is merged).
+// Hooks: what a launch that holds the consumer of the merged output adds
+// (NoAttnHooks: nothing). kNotify (with FUSED): the merged output is read later
+// in the same launch: it is stored device-coherently, and once a pair's merged
+// rows are performed thread 0 calls merged(a, live_pairs) (live_pairs counts
+// the (b, kv_head) pairs with keys; 1-64 sequences). no_units() runs on
+// workgroup 0 when no sequence has a key (then nothing is merged).
 struct NoAttnHooks {
-  static constexpr bool kWaitInput = false;
   static constexpr bool kNotify = false;
-  __device__ void wait_input() const {}
   __device__ void merged(const AttnArgs&, int) const {}
   __device__ void no_units() const {}
 };
@@ -230,7 +225,6 @@ template <bool QKV, int WM, bool FUSED, class Hooks = NoAttnHooks>
 __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
                                            const Hooks& hooks = Hooks{}) {
   static_assert(!Hooks::kNotify || FUSED, "a consumer in the launch reads the merged output");
-  static_assert(!Hooks::kWaitInput || QKV, "the in-launch producer writes qkv");
   __shared__ int lds_prev;
   __shared__ __align__(16) uint16_t lds_p[WM][G * 16];
   __shared__ __align__(16) float lds_acc[WM][4][G][D];  // [wave][key group g][head][col]
@@ -257,7 +251,6 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
   }
   if constexpr (Hooks::kNotify)
     if (total == 0 && wg == 0) hooks.no_units();
-  bool waited = false;
 
   for (int u = wg; u < total; u += nwg) {
     const int pidx = u / nkv;
@@ -324,16 +317,8 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       const bool do_k = new_unit && wave == (WM > G ? G : 0);  // the new key: an idle wavefront if any
       // 2 bf16 of a head row per lane
       auto ld_in = [&](const uint16_t* row) -> uint32_t {
-        uint32_t* p = const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(row)) + lane;
-        if constexpr (Hooks::kWaitInput)
-          return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-          return *p;
+        return reinterpret_cast<const uint32_t*>(row)[lane];
       };
-      if constexpr (Hooks::kWaitInput) {
-        if (!waited) hooks.wait_input();
-        waited = true;
-      }
       uint32_t xh[NH], xk = 0, kwv = 0, vv = 0;
 #pragma unroll
       for (int n = 0; n < NH; ++n) xh[n] = has_q ? ld_in(src + (kvh * G + wave + n * WM) * D) : 0u;
@@ -345,10 +330,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
         kwv = reinterpret_cast<const uint32_t*>(a.kw)[lane];
         vv = ld_in(src + (nq + nkv + kvh) * D);
       }
-      if (has_new) {
-        if constexpr (Hooks::kWaitInput) vnew = ldg16_coherent(src + (nq + nkv + kvh) * D + 8 * r);
-        else vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
-      }
+      if (has_new) vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
       asm volatile("" ::: "memory");  // keep every load above ahead of the first wait
       if (has_q) {
 #pragma unroll

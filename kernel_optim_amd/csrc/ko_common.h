@@ -51,13 +51,11 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // with a scalar base where possible, never to flat_load.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
-typedef const __attribute__((address_space(1))) uint32_t g_u32;
 
 __device__ __forceinline__ uint4 ldg16(const void* p) {
   const u32x4 v = *(g_u32x4*)p;
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ uint32_t ldg4(const void* p) { return *(g_u32*)p; }
 // Streaming load: the data is read exactly once, so mark it non-temporal.
 __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
   const u32x4 v = __builtin_nontemporal_load((g_u32x4*)p);
@@ -72,20 +70,6 @@ __device__ __forceinline__ uint4 ldg16_coherent(const void* p) {
   const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
-}
-
-// 8-byte relaxed agent-scope atomic load / store (global_load / global_store
-// ... sc1): data exchanged between workgroups of one launch.
-__device__ __forceinline__ uint2 ldg8_coherent(const void* p) {
-  const unsigned long long v = __hip_atomic_load(
-      reinterpret_cast<unsigned long long*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
-      __HIP_MEMORY_SCOPE_AGENT);
-  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-}
-__device__ __forceinline__ void stg8_coherent(void* p, uint2 v) {
-  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p),
-                     (unsigned long long)v.x | ((unsigned long long)v.y << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

@@ -34,7 +34,6 @@ import torch
 
 from .kernels.fused import DecodeAttention
 from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss, tile_weights
-from .kernels.layers import DecodeLayers
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
 
@@ -44,11 +43,9 @@ TUNE = os.environ.get("ENGINE_TUNE", "1") == "1"
 TUNE_BUDGET_S = 60.0
 # attention and the o projection in one launch for 1-2 sequences (ENGINE_FUSE_OPROJ=0: two)
 FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
-# B <= 2: every decoder layer of a step in one launch (kernels.layers.DecodeLayers);
-# off by default: on MI355X its stage hand-offs cost more than the launches they
-# replace (about 59 against 47 us per layer at batch 1)
-ONE_LAUNCH = os.environ.get("ENGINE_ONE_LAUNCH", "0") == "1"
 OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
+# keys per decode-attention unit (0: DecodeAttention's sizing rule)
+ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 
 
 def _rope_tables(n, d, theta, device):
@@ -134,13 +131,10 @@ class Engine:
                        else None)
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
-        self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
+        self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
+                                    unit=ATTN_UNIT or None, fused_combine=True)
         self.attn.oproj_delay_ns = OPROJ_DELAY_NS
         H, L = cfg.hidden, self.w["layers"]
-        self.dl = None
-        if ONE_LAUNCH and DecodeLayers.supported(self.attn, H, cfg.inter):
-            self.dl = DecodeLayers(self.attn, L, self.k_cache, self.v_cache, H, cfg.inter)
-            self.dl.o_delay_ns = OPROJ_DELAY_NS
         e = cfg.eps
         self.gv = dict(
             qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
@@ -154,9 +148,6 @@ class Engine:
         deadline = time.monotonic() + TUNE_BUDGET_S
         self.gw = {}
         for name, g in self.gv.items():
-            if self.dl is not None and name != "lm":  # the layers run in ko_decode_layers
-                self.gw[name] = raw[name]
-                continue
             tiled = None
             if any(c[0] == 2 for c in g.candidates()):
                 tiled = self._tiled(name, raw[name])
@@ -181,9 +172,7 @@ class Engine:
         g, W = self.gv, self.gw  # W: each projection's weights in its launch layout
         h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
         fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
-        if self.dl is not None:  # every layer in one launch
-            self.dl(h, self.qkv, self.attn_out, self.act, self.pos, self._cos, self._sin, cfg.eps)
-        for i, lw in enumerate(self.w["layers"] if self.dl is None else ()):
+        for i, lw in enumerate(self.w["layers"]):
             g["qkv"](h, W["qkv"][i], y=self.qkv, nw=lw["w_in"])
             if fuse_o:  # attention + o projection + residual in one launch
                 self.attn.decode_qkv_oproj(self.qkv, lw["q_norm"], lw["k_norm"], self._cos,
