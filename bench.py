@@ -150,7 +150,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     caches) are rotated so the Infinity Cache cannot serve a replay; the replays
     are captured in one graph and timed with events."""
     import torch
-    from kernel_optim_amd.kernels.fused import DecodeAttention
+    from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
     from kernel_optim_amd.kernels.gemv import EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, tile_weights
     from kernel_optim_amd.engine import _rope_tables
     from kernel_optim_amd.model import Qwen3Config, random_weights
@@ -170,7 +170,11 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         qkv = torch.empty(B, cfg.nqkv, device=dev, dtype=torch.bfloat16)
         att_out = torch.empty(B, cfg.nq * cfg.head_dim, device=dev, dtype=torch.bfloat16)
         act = torch.empty(B, cfg.inter, device=dev, dtype=torch.bfloat16)
-        att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
+        # the engine's decode step: fused combine, the step's RoPE rows once, and the
+        # o projection in the attention's launch where it fits (B <= 2)
+        att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
+        rope = torch.empty(B, 2, cfg.head_dim, device=dev, dtype=torch.bfloat16)
+        fuse_o = att.oproj_fusable()
         H = cfg.hidden
         L = w["layers"]
         e = cfg.eps
@@ -190,23 +194,30 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         def layer(i):
             lw = L[i]
             ops["qkv"](h, W["qkv"][i], y=qkv, nw=lw["w_in"])
-            att.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i], att_out,
-                           cfg.eps)
-            ops["o"](att_out, W["o"][i], h=h)
+            if fuse_o:
+                att.decode_qkv_oproj(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i],
+                                     att_out, cfg.eps, lw["o"], h, rope=rope)
+            else:
+                att.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i],
+                               att_out, cfg.eps, rope=rope)
+                ops["o"](att_out, W["o"][i], h=h)
             ops["gu"](h, W["gu"][i], y=act, nw=lw["w_post"])
             ops["down"](act, W["down"][i], h=h)
+
+        def layers():
+            rope_rows(pos, cos, sin, rope)
+            for i in range(nsets):
+                layer(i)
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for i in range(nsets):
-                layer(i)
+            layers()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for i in range(nsets):
-                layer(i)
+            layers()
         graph.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -72,13 +72,18 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
  * merge when counters != NULL, as for ko_decode_attn). Replaces the pair
  * qk_norm_rope (engine/kernels/fused.py:54-106) + DecodeAttention.__call__
  * (fused.py:221-234) as the reference's decode step calls them
- * (engine/engine.py:328-330). Positions must lie in [0, min(cap, max_pos)). */
+ * (engine/engine.py:328-330). Positions must lie in [0, min(cap, max_pos)).
+ * rope (optional, [B][2][head_dim] bf16, 16-byte aligned): the cos and sin rows
+ * at pos[b] as ko_rope_rows writes them; the kernel then reads them instead of
+ * the table rows behind the position, and for B == 1 (with a unit per
+ * workgroup) issues its first loads before it reads the position. */
 int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const void* cos,
                        const void* sin, int max_pos, const int* pos, void* k_cache,
                        void* v_cache, int cap, long long cache_b_stride,
                        long long cache_h_stride, int B, int nkv, int head_dim, int unit,
                        int max_units, int grid_waves, float eps, float scale, float* o_part,
-                       float* ml, int* counters, void* out, void* stream);
+                       float* ml, int* counters, void* out, const void* rope,
+                       void* stream);
 
 /* ko_decode_attn_qkv (with counters) and the o projection with its residual add
  * in ONE launch, for B <= 2 and unit % 64 == 0, unit < 1024 (4 wavefronts per
@@ -91,7 +96,8 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
  * the first call; every call leaves it zero); err [1] int32 is set to 1 if that
  * wait ever gave up (never expected; the results of such a call are invalid).
  * delay_ns: how long the projection workgroups hold their weight loads so the
- * attention's first loads go ahead of them (0: no delay). Replaces
+ * attention's first loads go ahead of them (0: no delay). rope: as for
+ * ko_decode_attn_qkv. Replaces
  * engine.py:328-332 (attention, o projection and its residual add); no single
  * reference function. */
 int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, const void* cos,
@@ -101,10 +107,18 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
                              int max_units, int grid_waves, float eps, float scale,
                              float* o_part, float* ml, int* counters, void* out,
                              const void* w_o, void* h, int H, int* sync, int* err,
-                             int delay_ns, void* stream);
+                             int delay_ns, const void* rope, void* stream);
 
 /* int32 elements of ko_decode_attn_qkv_oproj's sync array (a size, not a status). */
 long long ko_decode_attn_qkv_oproj_sync_ints(void);
+
+/* out[b] = (cos[p], sin[p]), p = clamp(pos[b], 0, rows - 1): each sequence's
+ * RoPE rows at its new position for the rope argument above (the rows that
+ * qk_norm_rope, engine/kernels/fused.py:71-87, reads). cos/sin [rows, d] bf16,
+ * out [B][2][d]; d % 8 == 0; 16-byte aligned. No reference counterpart: the
+ * reference reads the rows inside qk_norm_rope. */
+int ko_rope_rows(const int* pos, const void* cos, const void* sin, int rows, int d, int B,
+                 void* out, void* stream);
 
 /* ---- residual add + RMSNorm ---------------------------------------------
  * Replaces engine/kernels/fused.py:16-36 (_add_rms_norm_kernel) as launched by

@@ -605,14 +605,14 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
                        void* v_cache, int cap, long long cache_b_stride,
                        long long cache_h_stride, int B, int nkv, int head_dim, int unit,
                        int max_units, int grid_waves, float eps, float scale, float* o_part,
-                       float* ml, int* counters, void* out, void* stream) {
+                       float* ml, int* counters, void* out, const void* rope, void* stream) {
   int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
                         head_dim, unit, max_units, o_part, ml);
   if (st) return st;
   if (!qkv || !q_w || !k_w || !cos || !sin || !out || max_pos < 1 || grid_waves < 1)
     return KO_EINVAL;
   if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
-      !aligned16(sin) || !aligned16(out))
+      !aligned16(sin) || !aligned16(out) || (rope && !aligned16(rope)))
     return KO_EINVAL;
   AttnArgs a = base_args(k_cache, v_cache, pos, 1, cap, cache_b_stride, cache_h_stride, B, nkv,
                          unit, max_units, scale, o_part, ml);
@@ -625,6 +625,7 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
   a.max_pos = max_pos;
   a.counters = counters;
   a.out = static_cast<uint16_t*>(out);
+  a.rope = static_cast<const uint16_t*>(rope);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (counters) return launch1<true, true>(a, grid_waves, s);
   st = launch1<true, false>(a, grid_waves, s);
@@ -642,7 +643,7 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
                              int max_units, int grid_waves, float eps, float scale,
                              float* o_part, float* ml, int* counters, void* out,
                              const void* w_o, void* h, int H, int* sync, int* err,
-                             int delay_ns, void* stream) {
+                             int delay_ns, const void* rope, void* stream) {
   int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
                         head_dim, unit, max_units, o_part, ml);
   if (st) return st;
@@ -650,7 +651,8 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
       max_pos < 1 || grid_waves < 4 || H < 8 || (H & 7))
     return KO_EINVAL;
   if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
-      !aligned16(sin) || !aligned16(out) || !aligned16(w_o) || !aligned16(h))
+      !aligned16(sin) || !aligned16(out) || !aligned16(w_o) || !aligned16(h) ||
+      (rope && !aligned16(rope)))
     return KO_EINVAL;
   if (B > 2 || waves_per_unit(unit) != 4) return KO_ENOTSUP;
   const int K = nkv * G * D;  // o projection input width
@@ -667,6 +669,7 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
   a.counters = counters;
   a.out = static_cast<uint16_t*>(out);
   a.pairs_done = sync;
+  a.rope = static_cast<const uint16_t*>(rope);
   GemvArgs g = {};
   g.x = static_cast<const uint16_t*>(out);
   g.w = static_cast<const uint16_t*>(w_o);

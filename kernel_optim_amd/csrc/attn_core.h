@@ -47,6 +47,8 @@ struct AttnArgs {
   int* counters;         // [B*nkv] (FUSED)
   uint16_t* out;         // [B*T, nq*D] (FUSED)
   int* pairs_done;       // attention + o projection launch: merged (b, kv_head) pairs
+  const uint16_t* rope;  // [B][2][D]: cos and sin rows at each sequence's new position
+                         // (QKV; optional, else cosb / sinb at pos)
 };
 
 __device__ __forceinline__ int nunits(int len, int unit) {
@@ -240,9 +242,59 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
   const int sub = unit / WM;
   uint16_t* myp = lds_p[wave];
 
+  // Per-unit inputs. One query token, one sequence, the RoPE rows given and at
+  // most one unit per workgroup: this workgroup's unit u = wg is (c = wg / nkv,
+  // kv head wg % nkv) whatever the length, so its q-side loads and its first
+  // K/V step go out before the length is read (with the keys clamped to the
+  // cache instead of the length; keys past the length are masked and patched
+  // as with the length clamp, so the result is the same).
+  constexpr int NH = G / WM > 0 ? G / WM : 1;  // q heads normed per wavefront
+  constexpr int KW = WM > G ? G : 0;           // the wavefront that norms the new key
+  const int nqkv = (nq + 2 * nkv) * D;
+  uint4 ka[4], va[4];
+  uint32_t xh[NH], qwv = 0, cwv = 0, swv = 0, xk = 0, kwv = 0, vv = 0;
+  uint4 vnew = make_uint4(0, 0, 0, 0);
+  const bool spec = QKV && a.B == 1 && a.rope != nullptr && nwg >= nkv * max_units;
+  if (spec && wg < nkv * max_units) {
+    const int c = wg / nkv, kvh = wg - c * nkv;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.qkv);
+#pragma unroll
+    for (int n = 0; n < NH; ++n) xh[n] = wave < G ? src[(kvh * G + wave + n * WM) * (D / 2) + lane] : 0u;
+    qwv = reinterpret_cast<const uint32_t*>(a.qw)[lane];
+    cwv = reinterpret_cast<const uint32_t*>(a.rope)[lane];
+    swv = reinterpret_cast<const uint32_t*>(a.rope + D)[lane];
+    if (wave == KW) {
+      xk = src[(nq + kvh) * (D / 2) + lane];
+      kwv = reinterpret_cast<const uint32_t*>(a.kw)[lane];
+      vv = src[(nq + nkv + kvh) * (D / 2) + lane];
+    }
+    vnew = ldg16(a.qkv + (nq + nkv + kvh) * D + 8 * r);
+    const int k0 = c * unit + wave * sub;
+    if (k0 < a.cap) {
+      const int klim = min(k0 + sub, a.cap) - 1;
+      const uint16_t* kb = a.kc + (long long)kvh * a.ch;
+      const uint16_t* vb = a.vc + (long long)kvh * a.ch;
+      const uint16_t* p = kb + (long long)min(k0 + r, klim) * D + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ka[i] = ldg16_stream(p + 32 * i);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        va[s4] = ldg16_stream(vb + (long long)min(k0 + g + 4 * s4, klim) * D + 8 * r);
+    }
+  }
+
   const bool small_b = a.B <= 64;
-  int my_n = 0, my_incl = 0, total;
-  if (small_b) {
+  int my_n = 0, my_incl = 0, total, len1 = 0;
+  if (a.B == 1) {
+    // one sequence: its length through a scalar load (the constant address
+    // space), which waits on its own counter instead of queueing behind the
+    // vector loads above
+    const int len = *(const __attribute__((address_space(4))) int*)a.lens + a.len_off;
+    len1 = len < a.cap ? len : a.cap;
+    my_n = lane == 0 ? nunits(len1, unit) : 0;
+    my_incl = readlane(my_n, 0);
+    total = my_incl * nkv;
+  } else if (small_b) {
     my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap), unit) : 0;
     my_incl = wave_incl_scan(my_n);
     total = readlane(my_incl, 63) * nkv;
@@ -253,10 +305,15 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     if (total == 0 && wg == 0) hooks.no_units();
 
   for (int u = wg; u < total; u += nwg) {
+    const bool pre = spec && u == wg;  // this unit's first loads are in flight already
     const int pidx = u / nkv;
     const int kvh = u - pidx * nkv;
     int b, c, kv_len;
-    if (small_b) {
+    if (a.B == 1) {
+      b = 0;
+      c = pidx;
+      kv_len = len1;
+    } else if (small_b) {
       b = uniform(__popcll(__ballot(my_incl <= pidx)));
       c = pidx - readlane(my_incl - my_n, b);
       kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
@@ -299,38 +356,47 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
         vr[s4] = ldg16_stream(vb + (long long)key * D + 8 * r);
       }
     };
-    uint4 ka[4], va[4], kb2[4], vb2[4];
-    if (active) {
-      load_k(k0, ka);
-      load_v(k0, va);
-    }
+    // The first step's K/V loads go out after the q-side loads: loads return
+    // in issue order, so the q norm / RoPE then never waits for the K/V data.
+    uint4 kb2[4], vb2[4];
+    auto load_first_kv = [&] {
+      if (active && !pre) {
+        load_k(k0, ka);
+        load_v(k0, va);
+      }
+    };
 
     bf16x8 qa[4];
-    uint4 knew[4], vnew;
+    uint4 knew[4];
     if constexpr (QKV) {
       // q heads normed by each wavefront (wavefronts past the 4th norm none)
-      constexpr int NH = G / WM > 0 ? G / WM : 1;
       const bool has_q = wave < G;
-      const int nqkv = (nq + 2 * nkv) * D;
-      const int pt = min(max(pnew, 0), a.max_pos - 1);
       const uint16_t* src = a.qkv + (long long)b * nqkv;
-      const bool do_k = new_unit && wave == (WM > G ? G : 0);  // the new key: an idle wavefront if any
-      // 2 bf16 of a head row per lane
-      auto ld_in = [&](const uint16_t* row) -> uint32_t {
-        return reinterpret_cast<const uint32_t*>(row)[lane];
-      };
-      uint32_t xh[NH], xk = 0, kwv = 0, vv = 0;
+      const bool do_k = new_unit && wave == KW;  // the new key: an idle wavefront if any
+      if (!pre) {
+        // 2 bf16 of a head row per lane
+        auto ld_in = [&](const uint16_t* row) -> uint32_t {
+          return reinterpret_cast<const uint32_t*>(row)[lane];
+        };
 #pragma unroll
-      for (int n = 0; n < NH; ++n) xh[n] = has_q ? ld_in(src + (kvh * G + wave + n * WM) * D) : 0u;
-      const uint32_t qwv = reinterpret_cast<const uint32_t*>(a.qw)[lane];
-      const uint32_t cwv = reinterpret_cast<const uint32_t*>(a.cosb + (long long)pt * D)[lane];
-      const uint32_t swv = reinterpret_cast<const uint32_t*>(a.sinb + (long long)pt * D)[lane];
-      if (do_k) {
-        xk = ld_in(src + (nq + kvh) * D);
-        kwv = reinterpret_cast<const uint32_t*>(a.kw)[lane];
-        vv = ld_in(src + (nq + nkv + kvh) * D);
+        for (int n = 0; n < NH; ++n) xh[n] = has_q ? ld_in(src + (kvh * G + wave + n * WM) * D) : 0u;
+        qwv = reinterpret_cast<const uint32_t*>(a.qw)[lane];
+        if (a.rope) {
+          cwv = reinterpret_cast<const uint32_t*>(a.rope + (long long)b * 2 * D)[lane];
+          swv = reinterpret_cast<const uint32_t*>(a.rope + (long long)b * 2 * D + D)[lane];
+        } else {
+          const int pt = min(max(pnew, 0), a.max_pos - 1);
+          cwv = reinterpret_cast<const uint32_t*>(a.cosb + (long long)pt * D)[lane];
+          swv = reinterpret_cast<const uint32_t*>(a.sinb + (long long)pt * D)[lane];
+        }
+        if (do_k) {
+          xk = ld_in(src + (nq + kvh) * D);
+          kwv = reinterpret_cast<const uint32_t*>(a.kw)[lane];
+          vv = ld_in(src + (nq + nkv + kvh) * D);
+        }
+        if (has_new) vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
       }
-      if (has_new) vnew = ldg16(src + (nq + nkv + kvh) * D + 8 * r);
+      load_first_kv();
       asm volatile("" ::: "memory");  // keep every load above ahead of the first wait
       if (has_q) {
 #pragma unroll
@@ -358,6 +424,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       uint4 qv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) qv[i] = ldg16(qrow + 32 * i);
+      load_first_kv();
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, qv[i]);

@@ -221,9 +221,35 @@ __global__ __launch_bounds__(NT) void embed_ss_kernel(const long long* __restric
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The decode attention's RoPE rows: out[b] = (cos[p], sin[p]) with
+// p = clamp(pos[b], 0, rows - 1), the rows qk_norm_rope reads for the new
+// token (fused.py:71-87). One workgroup per sequence, 16-byte copies.
+__global__ __launch_bounds__(64) void rope_rows_kernel(const int* __restrict__ pos,
+                                                      const uint16_t* __restrict__ cosb,
+                                                      const uint16_t* __restrict__ sinb, int rows,
+                                                      int d, uint16_t* __restrict__ out) {
+  const int b = blockIdx.x;
+  const int p = min(max(pos[b], 0), rows - 1);
+  const int chunks = d / 8;  // per row
+  for (int i = threadIdx.x; i < 2 * chunks; i += blockDim.x) {
+    const uint16_t* src = (i < chunks ? cosb : sinb) + (long long)p * d + 8 * (i % chunks);
+    *reinterpret_cast<uint4*>(out + (long long)b * 2 * d + 8 * i) = ldg16(src);
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int ko_rope_rows(const int* pos, const void* cos, const void* sin, int rows, int d, int B,
+                 void* out, void* stream) {
+  if (!pos || !cos || !sin || !out || rows < 1 || B < 1 || d < 8 || (d & 7)) return KO_EINVAL;
+  if (((uintptr_t)cos | (uintptr_t)sin | (uintptr_t)out) & 15) return KO_EINVAL;
+  hipLaunchKernelGGL(rope_rows_kernel, dim3(B), dim3(64), 0, static_cast<hipStream_t>(stream), pos,
+                     static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), rows,
+                     d, static_cast<uint16_t*>(out));
+  return KO_LAUNCH_STATUS();
+}
 
 int ko_add_rms_norm(void* res, const void* delta, const void* weight, void* out, int rows, int n,
                     float eps, void* stream) {

@@ -32,7 +32,7 @@ import time
 
 import torch
 
-from .kernels.fused import DecodeAttention
+from .kernels.fused import DecodeAttention, rope_rows
 from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss, tile_weights
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
@@ -127,6 +127,7 @@ class Engine:
         self.q1 = torch.zeros(B, cfg.nq * cfg.head_dim, dtype=bf, device=dev)
         self.attn_out = torch.zeros_like(self.q1)
         self.act = torch.zeros(B, cfg.inter, dtype=bf, device=dev)
+        self.rope = torch.zeros(B, 2, cfg.head_dim, dtype=bf, device=dev)
         self.logits = (torch.zeros(B, cfg.vocab, dtype=bf, device=dev) if self.keep_logits
                        else None)
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
@@ -172,16 +173,17 @@ class Engine:
         g, W = self.gv, self.gw  # W: each projection's weights in its launch layout
         h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
         fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
+        rope_rows(self.pos, self._cos, self._sin, self.rope)  # the step's RoPE rows, once
         for i, lw in enumerate(self.w["layers"]):
             g["qkv"](h, W["qkv"][i], y=self.qkv, nw=lw["w_in"])
             if fuse_o:  # attention + o projection + residual in one launch
                 self.attn.decode_qkv_oproj(self.qkv, lw["q_norm"], lw["k_norm"], self._cos,
                                            self._sin, self.pos, self.k_cache[i], self.v_cache[i],
-                                           self.attn_out, cfg.eps, lw["o"], h)
+                                           self.attn_out, cfg.eps, lw["o"], h, rope=self.rope)
             else:
                 self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
                                      self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
-                                     cfg.eps)
+                                     cfg.eps, rope=self.rope)
                 g["o"](self.attn_out, W["o"][i], h=h)
             g["gu"](h, W["gu"][i], y=self.act, nw=lw["w_post"])
             g["down"](self.act, W["down"][i], h=h)

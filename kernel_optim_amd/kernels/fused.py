@@ -143,11 +143,17 @@ class DecodeAttention:
         return (self.B <= 2 and self.counters is not None and self.waves_per_unit == 4
                 and self.nq * self.d <= 4096)
 
-    def decode_qkv_oproj(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, w_o, h):
+    def _check_rope(self, rope):
+        if rope is not None:
+            _check(rope, "rope", BF16, (self.B, 2, self.d))
+
+    def decode_qkv_oproj(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, w_o, h,
+                         rope=None):
         """decode_qkv and then the o projection with its residual add, in one launch:
         out as decode_qkv leaves it, and h <- bf16(h + bf16(out @ w_o^T)) (the RESID
         GEMV of engine.py:330-331). The projection's weights stream while the
-        attention runs. w_o: [H, nq*d] bf16; h: [B, H] bf16."""
+        attention runs. w_o: [H, nq*d] bf16; h: [B, H] bf16; rope: as for
+        decode_qkv."""
         B, nq, nkv, d = self.B, self.nq, self.nkv, self.d
         _need(self.oproj_fusable(), "decode_qkv_oproj needs B <= 2, fused_combine and a unit "
                                     "of 4 wavefronts")
@@ -164,19 +170,23 @@ class DecodeAttention:
         _check(h, "h", BF16, (B, H))
         _check(w_o, "w_o", BF16, (H, nq * d))
         self._check_kv(k_cache, v_cache, pos)
+        self._check_rope(rope)
         _lib.call("ko_decode_attn_qkv_oproj", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w),
                   _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], _lib.ptr(pos), _lib.ptr(k_cache),
                   _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
                   self.unit, self.max_units, self.grid_waves, eps, self.scale,
                   _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters), _lib.ptr(out),
                   _lib.ptr(w_o), _lib.ptr(h), H, _lib.ptr(self.sync), _lib.ptr(self.err),
-                  self.oproj_delay_ns, _lib.stream_ptr())
+                  self.oproj_delay_ns, _lib.ptr(rope), _lib.stream_ptr())
 
-    def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps):
+    def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, rope=None):
         """Decode step (T=1) straight from the bf16 QKV projection [B, (nq+2nkv)*d]:
         per-head q/k RMSNorm + RoPE at pos[b], append of k and v at slot pos[b], and
         attention over keys 0..pos[b] -- qk_norm_rope (fused.py:54-96) and this
-        op's __call__ with the q/k work folded into the attention launch."""
+        op's __call__ with the q/k work folded into the attention launch.
+        ``rope`` ([B, 2, d] bf16, optional): the cos and sin rows at pos[b], as
+        ``rope_rows`` writes them; with it the kernel needs no table lookup behind
+        the position (and at B = 1 issues its first loads before reading it)."""
         B, nq, nkv, d = self.B, self.nq, self.nkv, self.d
         _need(self.T == 1, "decode_qkv serves one decode token per sequence")
         _check(qkv, "qkv", BF16, (B, (nq + 2 * nkv) * d))
@@ -188,12 +198,30 @@ class DecodeAttention:
         _need(cos.dim() == 2 and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape),
               "cos/sin must be [rows, d]")
         self._check_kv(k_cache, v_cache, pos)
+        self._check_rope(rope)
         _lib.call("ko_decode_attn_qkv", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w),
                   _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], _lib.ptr(pos), _lib.ptr(k_cache),
                   _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
                   self.unit, self.max_units, self.grid_waves, eps, self.scale,
                   _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters),
-                  _lib.ptr(out), _lib.stream_ptr())
+                  _lib.ptr(out), _lib.ptr(rope), _lib.stream_ptr())
+
+
+def rope_rows(pos, cos, sin, out):
+    """out[b] = (cos[p], sin[p]) with p = clamp(pos[b], 0, rows - 1): the RoPE rows
+    of each sequence's new position (qk_norm_rope, fused.py:71-87, reads the same
+    rows), written once per decode step for DecodeAttention's ``rope`` argument.
+    pos: [B] int32; cos/sin: [rows, d] bf16; out: [B, 2, d] bf16."""
+    _check(pos, "pos", torch.int32)
+    _need(pos.dim() == 1, "pos must be [B]")
+    B = pos.shape[0]
+    _check(cos, "cos", BF16)
+    _check(sin, "sin", BF16)
+    _need(cos.dim() == 2 and tuple(sin.shape) == tuple(cos.shape), "cos/sin must be [rows, d]")
+    d = cos.shape[1]
+    _check(out, "out", BF16, (B, 2, d))
+    _lib.call("ko_rope_rows", _lib.ptr(pos), _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], d, B,
+              _lib.ptr(out), _lib.stream_ptr())
 
 
 # ---------------------------------------------------------------------------

@@ -239,12 +239,63 @@ def test_decode_qkv_matches_norm_rope_append_then_attention(dev, B, cap, unit, f
     assert torch.equal(v.cpu(), vref)
 
 
+def test_rope_rows_are_the_table_rows(dev):
+    """rope_rows copies cos[p], sin[p] for each sequence's position, with p clamped
+    to the table."""
+    from oracle import ops as O
+    fused_mod = _fused()
+    cos, sin = (t.to(dev) for t in O.rope_tables(300, 128, 1.0e6))
+    pos = torch.tensor([0, 17, 299, 4000, -3], dtype=torch.int32, device=dev)
+    out = torch.full((5, 2, 128), 7.0, device=dev, dtype=torch.bfloat16)
+    fused_mod.rope_rows(pos, cos, sin, out)
+    torch.cuda.synchronize()
+    p = pos.clamp(0, 299).long()
+    assert torch.equal(out[:, 0], cos[p]) and torch.equal(out[:, 1], sin[p])
+
+
+@pytest.mark.parametrize("B,cap,pos0,unit", [(1, 1296, 1024, None), (1, 1296, 0, None),
+                                             (1, 1296, 1295, None), (1, 1296, 700, 256),
+                                             (1, 8192, 5000, 1024), (2, 640, 517, None)])
+def test_decode_qkv_with_rope_rows_is_bit_equal(dev, B, cap, pos0, unit):
+    """The attention with the step's RoPE rows passed in (and, at B = 1, its first
+    loads issued before the position is read, keys clamped to the cache) equals
+    the table-lookup path bit for bit: output, appended K and V."""
+    from oracle import ops as O
+    fused_mod = _fused()
+    nq, nkv, d = 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(70 + B + pos0)
+    qkv = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
+    k0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    v0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    pos = torch.tensor([pos0, max(pos0 - 300, 0)][:B], dtype=torch.int32, device=dev)
+    res = []
+    for use_rope in (False, True):
+        att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, unit=unit, fused_combine=True)
+        k, v = k0.clone(), v0.clone()
+        out = torch.zeros(B, nq * d, device=dev, dtype=torch.bfloat16)
+        rope = None
+        if use_rope:
+            rope = torch.empty(B, 2, d, device=dev, dtype=torch.bfloat16)
+            fused_mod.rope_rows(pos, cos, sin, rope)
+        att.decode_qkv(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6, rope=rope)
+        torch.cuda.synchronize()
+        assert torch.all(att.counters == 0)
+        res.append((out.cpu(), k.cpu(), v.cpu()))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("B,cap,pos0", [(1, 1296, 1024), (1, 1296, 0), (2, 640, 517)])
 def test_decode_qkv_oproj_equals_attention_then_o_gemv(dev, B, cap, pos0):
     """The one-launch attention + o projection equals decode_qkv followed by the RESID
     GEMV (engine.py:328-331) bit for bit -- same merged attention rows, same
     dot-product order -- including the KV append, over several graph replays whose
-    positions advance (the launch re-arms its counters every time)."""
+    positions advance (the launch re-arms its counters every time). The one-launch
+    side takes the step's RoPE rows from rope_rows (inside the graph, as the
+    engine does), the other the tables."""
     from oracle import ops as O
     from kernel_optim_amd.kernels import gemv as GV
     fused_mod = _fused()
@@ -266,10 +317,13 @@ def test_decode_qkv_oproj_equals_attention_then_o_gemv(dev, B, cap, pos0):
         att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, fused_combine=True)
         o = GV.Gemv(B, H, nq * d, GV.EPI_RESID, norm=False)
         out = torch.zeros(B, nq * d, device=dev, dtype=torch.bfloat16)
+        rope = torch.zeros(B, 2, d, device=dev, dtype=torch.bfloat16)
 
         def step():
             if fused_launch:
-                att.decode_qkv_oproj(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6, w_o, h)
+                fused_mod.rope_rows(pos, cos, sin, rope)
+                att.decode_qkv_oproj(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6, w_o, h,
+                                     rope=rope)
             else:
                 att.decode_qkv(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6)
                 o(out, w_o, h=h, cfg=(0, 8, 0))
