@@ -38,6 +38,8 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true", help="skip the B1 decode measurement")
     ap.add_argument("--no-attn", action="store_true",
                     help="skip the attention measurement (profiling the decode step alone)")
+    ap.add_argument("--no-ragged", action="store_true",
+                    help="skip the ragged B=64 attention measurement (profiling B16 x 8K alone)")
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--new-tokens", type=int, default=256)
     ap.add_argument("--decode-b16", action="store_true",
@@ -136,6 +138,7 @@ def bench_decode(args, eng=None, B=1):
                      "achieved_gbs": round(step_bytes * tok_s / B / 1e9, 1),
                      "graph_step_frac": round((step_bytes / (step_ms * 1e-3) / 1e9) / PEAK_HBM_GBS, 4)},
         "first_tokens": out[:8],
+        "gemv_cfg": {k: [list(g.cfg), round(g.us, 2)] for k, g in eng.gv.items()},
     }
     if not args.no_cpu and B == 1:
         res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
@@ -344,7 +347,7 @@ def bench_attention(args):
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "wall_s_timed": round(wall, 4),
         "roofline": {"bound": "hbm",
-                     "kernel": f"attn1_kernel<false, {att.waves_per_unit}> (split-K partials)",
+                     "kernel": f"attn1_kernel<false, {att.waves_per_unit}, false> (split-K partials)",
                      "achieved": round(k_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
                      "avg_kernel_us": round(k_ms * 1e3, 3),
@@ -415,7 +418,7 @@ def main():
             line["decode_b16"] = bench_decode(args, eng, B=16)
         del eng
         torch.cuda.empty_cache()
-    if not args.no_attn:
+    if not args.no_attn and not args.no_ragged:
         line["attention_ragged_b64"] = bench_attention_ragged()
     if args.layer:
         line["layer_2048"] = bench_layer()

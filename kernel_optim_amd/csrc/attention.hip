@@ -523,7 +523,6 @@ int launch1_wm(const AttnArgs& a, int grid_waves, hipStream_t s) {
 template <bool QKV, bool FUSED>
 int launch1(const AttnArgs& a, int grid_waves, hipStream_t s) {
   switch (waves_per_unit(a.unit)) {
-    case 8: return launch1_wm<QKV, 8, FUSED>(a, grid_waves, s);
     case 4: return launch1_wm<QKV, 4, FUSED>(a, grid_waves, s);
     case 2: return launch1_wm<QKV, 2, FUSED>(a, grid_waves, s);
     default: return launch1_wm<QKV, 1, FUSED>(a, grid_waves, s);

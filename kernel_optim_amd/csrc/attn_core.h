@@ -650,12 +650,11 @@ inline int check_common(const void* kc, const void* vc, const int* lens, int cap
   return KO_OK;
 }
 
-// Wavefronts per workgroup of attn1_kernel for a unit size: 8 for long units
-// (>= 1024 keys, at least 8 steps per wavefront), else the largest of 4, 2, 1
-// that splits the unit into whole 16-key steps.
+// Wavefronts per workgroup of attn1_kernel for a unit size: the largest of 4,
+// 2, 1 that splits the unit into whole 16-key steps. (8 wavefronts per long
+// unit measured slower on MI355X: B16 x 8K partials 85.5 against 83.6 us.)
 
 inline int waves_per_unit(int unit) {
-  if (unit >= 1024 && unit % 128 == 0) return 8;
   return unit % 64 == 0 ? 4 : unit % 32 == 0 ? 2 : 1;
 }
 

@@ -61,8 +61,8 @@ class DecodeAttention:
     of ``grid_waves`` wavefronts strides over the units (graph-safe).
     ``target_ctas`` is the number of wavefronts to fill the GPU with
     (256 CUs x 8 by default). For one query token per sequence a unit is
-    shared by the wavefronts of a workgroup (4, or 8 for units of 1024+ keys,
-    merged in LDS), so the unit is 4x the per-wavefront share.
+    shared by the 4 wavefronts of a workgroup (merged in LDS), so the unit is
+    4x the per-wavefront share.
 
     A second launch merges the partials, as the reference does; with
     ``fused_combine`` the last unit of each (sequence, KV head) merges them in
@@ -90,8 +90,6 @@ class DecodeAttention:
         # wavefronts per unit: the kernel's rule (attention.hip, waves_per_unit)
         if not wg_split:
             wpu = 1
-        elif unit >= 1024 and unit % 128 == 0:
-            wpu = 8
         else:
             wpu = 4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1
         self.waves_per_unit = wpu
