@@ -200,6 +200,13 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
  * ko_gemv, no reference counterpart. */
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
 
+/* Replaces torch.argmax(logits, dim=-1, out=vout) of the speculative verify
+ * step (engine/engine.py:413-415): ids[m] = argmax_n x[m, n] over bf16 logits
+ * [M, N] with row stride ld elements (ld % 8 == 0, x 16-byte aligned), lowest
+ * index on ties. One workgroup per row; no memset, so it can be captured in a
+ * graph. */
+int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, void* stream);
+
 /* Re-lays a row-major bf16 weight w [rows, K] into the tiled layout of ko_gemv
  * layout 2: wt holds ceil(rows/16)*16*K elements; for row tile t and k step s
  * (32 columns) the 1 KiB block at element ((t * K/32 + s) * 64 + l) * 8 holds,

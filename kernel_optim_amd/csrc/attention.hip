@@ -205,13 +205,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     } else {
       const int trow = (r >> 2) % T;
       const uint16_t* qrow =
-          a.q + ((long long)(b * T + trow) * nq + kvh * G + (r & 3)) * D + 8 * g;
+          a.q + ((long long)(b * a.tstride + a.t0 + trow) * nq + kvh * G + (r & 3)) * D + 8 * g;
 #pragma unroll
       for (int i = 0; i < 4; ++i) qa[i] = __builtin_bit_cast(bf16x8, ldg16(qrow + 32 * i));
     }
 
     const int tq = g % T;                           // token of this lane's score rows
-    const int lim = min(k1, kv_len - T + tq + 1);   // exclusive causal key limit
+    // exclusive causal key limit: token t0 + tq of the call's tstride tokens
+    // sits at key position kv_len - tstride + t0 + tq
+    const int lim = min(k1, kv_len - a.tstride + a.t0 + tq + 1);
 
     float mu[T][G];
     float acc[T][G][8];
@@ -361,7 +363,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const long long R = (long long)(b * T + t) * nq + kvh * G + g;
+      const long long R = (long long)(b * a.tstride + a.t0 + t) * nq + kvh * G + g;
       float* dst = a.o_part + (R * max_units + c) * D + 8 * r;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
@@ -382,7 +384,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
           m = (g == t && r == j) ? mu[t][j] : m;
           l = (r == j) ? lrow[j] : l;
         }
-      const long long R = (long long)(b * T + g) * nq + kvh * G + r;
+      const long long R = (long long)(b * a.tstride + a.t0 + g) * nq + kvh * G + r;
       reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(m, l);
     }
 
@@ -401,8 +403,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (int t = 0; t < T; ++t)
 #pragma unroll
           for (int j = 0; j < G; ++j)
-            combine_row<32>(a.o_part, a.ml, (long long)(b * T + t) * nq + kvh * G + j, n, nullptr, 0,
-                        a.cap, unit, max_units, a.out);
+            combine_row<32>(a.o_part, a.ml, (long long)(b * a.tstride + a.t0 + t) * nq + kvh * G + j,
+                            n, nullptr, 0, a.cap, unit, max_units, a.out);
         if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -530,13 +532,32 @@ int launch1(const AttnArgs& a, int grid_waves, hipStream_t s) {
 }
 
 template <bool FUSED>
-int launch_t(const AttnArgs& a, int T, int grid_waves, hipStream_t s) {
-  switch (T) {
-    case 1: return launch1<false, FUSED>(a, grid_waves, s);
+int launch_tc(const AttnArgs& a, int tc, int grid_waves, hipStream_t s) {
+  switch (tc) {
     case 2: return launch<2, false, FUSED>(a, grid_waves, s);
     case 3: return launch<3, false, FUSED>(a, grid_waves, s);
     default: return launch<4, false, FUSED>(a, grid_waves, s);
   }
+}
+
+// T query tokens per sequence: T = 1 is the decode kernel; T = 2..4 one
+// launch of attn_kernel<T>; T = 5..8 two launches of 2-4 tokens each (5 =
+// 3 + 2, 6 = 3 + 3, 7 = 4 + 3, 8 = 4 + 4). Every launch covers the whole key
+// range of the call with the causal limit of its own tokens, so all have the
+// same units per pair and the merge of a row sees the unit count of the call.
+template <bool FUSED>
+int launch_t(AttnArgs a, int T, int grid_waves, hipStream_t s) {
+  if (T == 1) return launch1<false, FUSED>(a, grid_waves, s);
+  a.tstride = T;
+  const int n = (T + 3) / 4;
+  for (int i = 0, t0 = 0; i < n; ++i) {
+    const int tc = (T - t0 + (n - i) - 1) / (n - i);  // 2..4 tokens
+    a.t0 = t0;
+    const int st = launch_tc<FUSED>(a, tc, grid_waves, s);
+    if (st) return st;
+    t0 += tc;
+  }
+  return KO_OK;
 }
 
 

@@ -26,6 +26,8 @@ constexpr int SPIN_MAX = 1 << 21;
 constexpr int OPROJ_FLAG0 = 32, OPROJ_FLAG_STRIDE = 32, OPROJ_FLAGS = 32;
 constexpr int OPROJ_SYNC_INTS = OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * OPROJ_FLAGS;
 
+constexpr int MAX_T = 8;  // query tokens per sequence of one attention call
+
 struct AttnArgs {
   const uint16_t* q;     // [B*T, nq*D] (unless QKV)
   const uint16_t* qkv;   // [B, (nq+2nkv)*D] (QKV)
@@ -41,6 +43,11 @@ struct AttnArgs {
   int len_off, cap;
   long long cb, ch;
   int B, nkv, unit, max_units;
+  // Query tokens per sequence in the q / out / partial row layout (T of the
+  // call), and the first token this launch serves: calls of more than 4
+  // tokens run in launches of up to 4 (attn_kernel's tile holds 4 tokens x 4
+  // heads).
+  int tstride, t0;
   float scale_log2;
   float* o_part;
   float* ml;
@@ -641,7 +648,7 @@ inline int check_common(const void* kc, const void* vc, const int* lens, int cap
                  const float* o_part, const float* ml) {
   if (!kc || !vc || !lens || !o_part || !ml) return KO_EINVAL;
   if (head_dim != D) return KO_ENOTSUP;
-  if (T < 1 || T > 4) return KO_ENOTSUP;
+  if (T < 1 || T > MAX_T) return KO_ENOTSUP;
   if (B < 1 || nkv < 1 || cap < 1) return KO_EINVAL;
   if (unit < 16 || (unit & 15)) return KO_EINVAL;
   if ((long long)max_units * unit < cap) return KO_ERANGE;
@@ -677,6 +684,8 @@ inline AttnArgs base_args(const void* k_cache, const void* v_cache, const int* l
   a.o_part = o_part;
   a.ml = ml;
   a.max_pos = 1;
+  a.tstride = 1;
+  a.t0 = 0;
   return a;
 }
 

@@ -625,6 +625,64 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
   }
 }
 
+// Greedy id of each row of bf16 logits [M, N] (row stride ld elements): one
+// 1024-thread workgroup per row, lowest index on ties (torch.argmax over the
+// verify step's logits, engine.py:413-415). Every thread reads 8 columns per
+// 16-byte load, AL loads in flight before it compares; a scalar tail covers N
+// not a multiple of 8.
+constexpr int AL = 8;
+__global__ __launch_bounds__(FT) void argmax_rows_kernel(const uint16_t* __restrict__ x,
+                                                         long long ld, int N,
+                                                         long long* __restrict__ ids) {
+  __shared__ float2 s_best[FT / 64];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const uint16_t* row = x + (long long)m * ld;
+  const int nc = N >> 3;  // whole 8-column chunks
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int c0 = t; c0 < nc; c0 += AL * FT) {
+    uint4 u[AL];
+#pragma unroll
+    for (int j = 0; j < AL; ++j) {
+      const int c = c0 + j * FT;
+      u[j] = c < nc ? ldg16(row + 8 * c) : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u,
+                                                      0xff80ff80u);  // -inf
+    }
+#pragma unroll
+    for (int j = 0; j < AL; ++j) {
+      const int base = 8 * (c0 + j * FT);
+      const uint32_t w[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        better(bf16lo(w[e]), base + 2 * e, bv, bi);
+        better(bf16hi(w[e]), base + 2 * e + 1, bv, bi);
+      }
+    }
+  }
+  for (int c = 8 * nc + t; c < N; c += FT) better(bf16lo(row[c]), c, bv, bi);
+#define KO_ROW_STEP(CTRL)                                                                   \
+  {                                                                                         \
+    const float ov = dpp_f<CTRL>(bv);                                                       \
+    const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xf, 0xf, false);               \
+    better(ov, oi, bv, bi);                                                                 \
+  }
+  KO_ROW_STEP(0x128)
+  KO_ROW_STEP(0x124)
+  KO_ROW_STEP(0x122)
+  KO_ROW_STEP(0x121)
+#undef KO_ROW_STEP
+  better_xor16(bv, bi);
+  better_xor32(bv, bi);
+  if (lane == 0) s_best[wv] = make_float2(bv, __int_as_float(bi));
+  __syncthreads();
+  if (t == 0) {
+    float v = s_best[0].x;
+    int i = __float_as_int(s_best[0].y);
+    for (int w = 1; w < FT / 64; ++w) better(s_best[w].x, __float_as_int(s_best[w].y), v, i);
+    ids[m] = i;
+  }
+}
+
 template <int M, int R, int CPT>
 int launch_row(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
   const dim3 grid((a.N + R - 1) / R), block(NT);
@@ -859,6 +917,13 @@ int ko_gemv_tile(const void* w, void* wt, int rows, int K, void* stream) {
   hipLaunchKernelGGL(gemv_tile_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w),
                      static_cast<uint16_t*>(wt), rows, K, nchunks);
+  return KO_LAUNCH_STATUS();
+}
+
+int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, void* stream) {
+  if (!x || !ids || M < 1 || N < 1 || ld < N || (ld & 7) || !al16(x)) return KO_EINVAL;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(M), dim3(FT), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), ld, N, ids);
   return KO_LAUNCH_STATUS();
 }
 

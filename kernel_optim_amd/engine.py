@@ -24,6 +24,15 @@ and after the layers the LM head with the greedy argmax fused into it; its
 finalize kernel also advances the positions and gathers the chosen tokens'
 embedding rows, the next step's input. Replays are pipelined: the next step is queued before
 the host waits for the previous step's ids (engine.py:509-522).
+
+With ENGINE_SPEC=1 (off by default, as in the reference, engine.py:40-42) the
+engine also drafts tokens by prompt lookup (NgramIndex) and checks them with a
+second captured graph, the verify step: B*(K+1) rows through the same layers,
+attention causal within each sequence's block, greedy ids at every row. The
+longest agreeing prefix plus the model's own next token is accepted per
+sequence; when the accepted tokens per verify step fall below the measured
+break-even, decoding finishes on the pipelined one-token graph
+(engine.py:403-508).
 """
 
 import os
@@ -32,8 +41,9 @@ import time
 
 import torch
 
-from .kernels.fused import DecodeAttention, rope_rows
-from .kernels.gemv import EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, embed_ss, tile_weights
+from .kernels.fused import DecodeAttention, add_rms_norm, qk_norm_rope, rope_rows, silu_mul
+from .kernels.gemv import (EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, argmax_rows,
+                           embed_ss, tile_weights)
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
 
@@ -46,6 +56,76 @@ FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
 OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
+# speculative decoding by prompt lookup (engine.py:35-57)
+SPEC = os.environ.get("ENGINE_SPEC", "0") == "1"
+NGRAMS = (3, 2, 1)       # lookup order: the longest suffix first
+WINDOW = 8               # verify steps between two acceptance checks
+HOST_MS = 0.2            # host time per verify step (wait, draft, copies)
+MIN_ADVANCE = (float(os.environ["ENGINE_MIN_ADVANCE"]) if "ENGINE_MIN_ADVANCE" in os.environ
+               else None)
+FUSED_VERIFY_ROWS = 16   # verify rows the fused GEMVs take in one weight pass
+
+
+def draft_len(B):
+    """Drafted tokens per sequence and verify step (engine.py:48-57): the verify
+    rows B*(K+1) stay few enough to be weight-streaming bound."""
+    if B <= 4:
+        return 6
+    if B <= 16:
+        return 4
+    if B <= 32:
+        return 2
+    return 0
+
+
+class NgramIndex:
+    """Prompt-lookup drafts for one sequence (the reference's _Lookup,
+    engine.py:60-93). ``after[n]`` maps every n-gram of the sequence that has a
+    successor to the index of that successor at its latest occurrence; a draft
+    follows the latest earlier occurrence of the sequence's last 3, else 2,
+    else 1 tokens, and repeats the last token when none occurred before."""
+
+    def __init__(self, tokens):
+        self.seq = []
+        self.after = {n: {} for n in NGRAMS}
+        self.extend(tokens)
+
+    def extend(self, tokens):
+        seq = self.seq
+        for t in tokens:
+            i = len(seq)        # t succeeds the n-grams that end at i - 1
+            seq.append(int(t))
+            for n in NGRAMS:
+                if i >= n:
+                    self.after[n][tuple(seq[i - n:i])] = i
+
+    def draft(self, K):
+        seq = self.seq
+        L = len(seq)
+        for n in NGRAMS:
+            if L < n:
+                continue
+            j = self.after[n].get(tuple(seq[L - n:]))
+            if j is None:
+                continue
+            out = []
+            for k in range(K):
+                # past the end the continuation reads the draft itself (a loop)
+                out.append(seq[j + k] if j + k < L else out[j + k - L])
+            return out
+        return [seq[-1]] * K
+
+
+def accept(draft_row, got_row):
+    """Tokens accepted from one verify row (engine.py:477-484): draft_row is the
+    verified input [last, d_1..d_K], got_row the greedy ids at those positions;
+    the drafts agree while d_{i+1} == got_i, and the model's next token follows
+    the agreeing prefix."""
+    K = len(draft_row) - 1
+    a = 0
+    while a < K and draft_row[a + 1] == got_row[a]:
+        a += 1
+    return list(got_row[:a + 1])
 
 
 def _rope_tables(n, d, theta, device):
@@ -66,7 +146,7 @@ def _log(msg):
 
 
 class Engine:
-    def __init__(self, model_path: str, keep_logits: bool = False) -> None:
+    def __init__(self, model_path: str, keep_logits: bool = False, spec=None) -> None:
         self._t0 = time.monotonic()
         if model_path.startswith("random"):
             seed = int(model_path.split(":", 1)[1]) if ":" in model_path else 0
@@ -78,18 +158,22 @@ class Engine:
         else:
             cfg = Qwen3Config.from_hf_json(os.path.join(model_path, "config.json"))
             w = random_weights(cfg, seed=int(os.environ.get("ENGINE_SEED", "0")), device=DEVICE)
-        self._init(cfg, w, keep_logits)
+        self._init(cfg, w, keep_logits, spec)
 
     @classmethod
-    def from_weights(cls, cfg, weights, keep_logits=False):
+    def from_weights(cls, cfg, weights, keep_logits=False, spec=None):
         """Engine over weights already in the decode layout (moved to the GPU)."""
         from .model import weights_to
         self = cls.__new__(cls)
         self._t0 = time.monotonic()
-        self._init(cfg, weights_to(weights, DEVICE), keep_logits)
+        self._init(cfg, weights_to(weights, DEVICE), keep_logits, spec)
         return self
 
-    def _init(self, cfg, w, keep_logits):
+    def _init(self, cfg, w, keep_logits, spec=None):
+        """spec: prompt-lookup speculation on (True) or off (False); None takes
+        ENGINE_SPEC (off unless set to 1)."""
+        self.spec = SPEC if spec is None else bool(spec)
+        self.min_advance = MIN_ADVANCE   # None: the measured break-even
         if cfg.head_dim != 128 or cfg.nq != 4 * cfg.nkv:
             raise ValueError("the decode kernels serve head_dim 128 with 4 query heads per KV head")
         self.cfg, self.w = cfg, w
@@ -109,11 +193,14 @@ class Engine:
         if self._shape == key:
             return
         self._shape = None
-        self.g1 = None
+        self.g1 = self.gk = None
         self.k_cache = self.v_cache = None
         torch.cuda.empty_cache()
         cfg = self.cfg
-        cap = -(-(S + N + 1) // 16) * 16
+        self.K = draft_len(B) if self.spec and N > 2 else 0
+        # with speculation a sequence can run ahead of the slowest by N + K tokens
+        need = S + 2 * N + 2 * self.K + 2 if self.K else S + N + 1
+        cap = -(-need // 16) * 16
         self.B, self.S, self.cap = B, S, cap
         self._tables(cap)
         dev = DEVICE
@@ -157,7 +244,76 @@ class Engine:
                 _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
             self.gw[name] = tiled if g.cfg[0] == 2 else raw[name]
         self.g1 = self._capture(self._step1)
+        self.gk = None
+        if self.K:
+            self._setup_verify(raw, deadline)
         self._shape = key
+
+    def _setup_verify(self, raw, deadline):
+        """Buffers, GEMVs and the captured graph of the verify step, and the
+        break-even tokens per verify step (engine.py:209-223)."""
+        cfg, B, dev, bf = self.cfg, self.B, DEVICE, torch.bfloat16
+        T = self.K + 1
+        M = B * T
+        H, e = cfg.hidden, cfg.eps
+        self.T = T
+        self.vin = torch.zeros(B, T, dtype=torch.int64, device=dev)
+        self.vout = torch.zeros(B, T, dtype=torch.int64, device=dev)
+        self.pin_vin = torch.empty(B, T, dtype=torch.int64, pin_memory=True)
+        self.pin_vout = torch.empty(B, T, dtype=torch.int64, pin_memory=True)
+        self.pin_pos = torch.empty(B, dtype=torch.int32, pin_memory=True)
+        self.hT = torch.zeros(M, H, dtype=bf, device=dev)
+        self.qkvT = torch.zeros(M, cfg.nqkv, dtype=bf, device=dev)
+        self.qT = torch.zeros(M, cfg.nq * cfg.head_dim, dtype=bf, device=dev)
+        self.attT = torch.zeros_like(self.qT)
+        self.actT = torch.zeros(M, cfg.inter, dtype=bf, device=dev)
+        self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
+                                     fused_combine=True)
+        self.verify_fused = M <= FUSED_VERIFY_ROWS
+        if self.verify_fused:   # one weight pass per projection on the fused GEMVs
+            self.gvk = dict(
+                qkv=Gemv(M, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
+                o=Gemv(M, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
+                gu=Gemv(M, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
+                down=Gemv(M, H, cfg.inter, EPI_RESID, norm=False, eps=e),
+                lm=Gemv(M, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
+            )
+            self.gwk = {}
+            for name, g in self.gvk.items():
+                tiled = None
+                if any(c[0] == 2 for c in g.candidates()):
+                    tiled = self._tiled(name, raw[name])
+                if TUNE:
+                    g.tune(raw[name], deadline, tiled=tiled)
+                    _log(f"verify gemv {name} M={M} cfg={g.cfg} {g.us:.1f}us")
+                self.gwk[name] = tiled if g.cfg[0] == 2 else raw[name]
+        else:                   # hipBLASLt GEMMs between the fused ops
+            self.nT = torch.zeros(M, H, dtype=bf, device=dev)
+            self.guT = torch.zeros(M, 2 * cfg.inter, dtype=bf, device=dev)
+        self.logitsT = (torch.zeros(M, cfg.vocab, dtype=bf, device=dev)
+                        if self.keep_logits or not self.verify_fused else None)
+        self.gk = self._capture(self._stepk)
+        t1 = min(self._time_graph(self.g1) for _ in range(2))
+        tk = min(self._time_graph(self.gk) for _ in range(2))
+        self.t_step_ms, self.t_verify_ms = t1, tk
+        self.breakeven = (tk + HOST_MS) / t1 if self.min_advance is None else self.min_advance
+        _log(f"B={B} K={self.K}: step {t1 * 1e3:.0f}us verify {tk * 1e3:.0f}us -> speculate "
+             f"while >= {self.breakeven:.3f} tokens/step")
+
+    def _time_graph(self, g, reps=10):
+        """Mean replay time (ms) of a captured step from positions where every
+        cache write stays inside the capacity."""
+        start = max(0, min(self.S, self.cap - (reps + 2) - (self.K + 1)))
+        torch.cuda.synchronize()
+        self.pos.fill_(start)
+        g.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
 
     def _tiled(self, name, weights):
         """MFMA-layout copies of one projection's weights (kernels.gemv.tile_weights),
@@ -189,6 +345,45 @@ class Engine:
             g["down"](self.act, W["down"][i], h=h)
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
                 pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
+
+    def _stepk(self):
+        """Verify step (engine.py:403-416): vin[b] = [last accepted token, K drafts]
+        at positions pos[b] .. pos[b]+K, through every layer as B*(K+1) rows (K/V
+        appended at those slots, attention causal within the block); vout[b, t]
+        = greedy id after vin[b, :t+1]. Positions do not advance."""
+        cfg = self.cfg
+        T = self.T
+        eps = cfg.eps
+        h = self.hT
+        embed_ss(self.vin.view(-1), self.w["embed"], h, None)
+        fused = self.verify_fused
+        g, W = (self.gvk, self.gwk) if fused else (None, None)
+        for i, lw in enumerate(self.w["layers"]):
+            if fused:
+                g["qkv"](h, W["qkv"][i], y=self.qkvT, nw=lw["w_in"])
+            else:
+                add_rms_norm(h, None, lw["w_in"], self.nT, eps)
+                torch.mm(self.nT, lw["qkv"].t(), out=self.qkvT)
+            qk_norm_rope(self.qkvT, lw["q_norm"], lw["k_norm"], self._cos, self._sin, self.pos,
+                         self.qT, self.k_cache[i], self.v_cache[i], T, eps, cfg.nq, cfg.nkv,
+                         cfg.head_dim)
+            self.attnk(self.qT, self.k_cache[i], self.v_cache[i], self.pos, self.attT)
+            if fused:
+                g["o"](self.attT, W["o"][i], h=h)
+                g["gu"](h, W["gu"][i], y=self.actT, nw=lw["w_post"])
+                g["down"](self.actT, W["down"][i], h=h)
+            else:   # h <- bf16(h + bf16(x @ W^T)), the RESID chain
+                h.add_(torch.mm(self.attT, lw["o"].t()))
+                add_rms_norm(h, None, lw["w_post"], self.nT, eps)
+                torch.mm(self.nT, lw["gu"].t(), out=self.guT)
+                silu_mul(self.guT, self.actT)
+                h.add_(torch.mm(self.actT, lw["down"].t()))
+        if fused:
+            g["lm"](h, W["lm"][0], y=self.logitsT, nw=self.w["final_norm"], ids=self.vout.view(-1))
+        else:
+            add_rms_norm(h, None, self.w["final_norm"], self.nT, eps)
+            torch.mm(self.nT, self.w["lm_head"].t(), out=self.logitsT)
+            argmax_rows(self.logitsT, self.vout.view(-1))
 
     def _capture(self, fn):
         # Warm up on a side stream, then capture. Warm-up steps write cache slot 0,
@@ -224,6 +419,21 @@ class Engine:
         self.g1.replay()
 
     @torch.inference_mode()
+    def verify_step(self, rows, pos):
+        """Replay the verify graph for rows [B, K+1] (int64: the last accepted token
+        and K drafts) at positions pos [B] (of rows[:, 0]); returns the greedy ids
+        [B, K+1] and, with keep_logits, the bf16 logits [B*(K+1), V], on the CPU.
+        Writes K/V cache slots pos .. pos+K. Needs a setup with speculation."""
+        if self.gk is None:
+            raise ValueError("verify_step needs an engine set up with speculation (spec=True, "
+                             "max_new_tokens > 2, a batch of at most 32)")
+        self.vin.copy_(torch.as_tensor(rows, dtype=torch.int64))
+        self.pos.copy_(torch.as_tensor(pos, dtype=torch.int32))
+        self.gk.replay()
+        torch.cuda.synchronize()
+        return self.vout.cpu(), (self.logitsT.cpu() if self.keep_logits else None)
+
+    @torch.inference_mode()
     def time_step(self, reps=20):
         """Mean GPU time (ms) of one replayed decode step, from positions S."""
         torch.cuda.synchronize()
@@ -252,6 +462,9 @@ class Engine:
         ids_h, ev = self.pin_ids, self.events
         ids_h[0].copy_(self.ids, non_blocking=True)
         ev[0].record(stream)
+        if self.K:
+            yield from self._generate_spec(input_ids, N, stream)
+            return
         # Keep one replay in flight: queue step j before waiting for step j-1.
         if N > 1:
             self.g1.replay()
@@ -266,6 +479,84 @@ class Engine:
                 ev[j + 1].record(stream)
             ev[j].synchronize()
             yield ids_h[j].tolist()
+
+    def _generate_spec(self, input_ids, N, stream):
+        """generate() with prompt-lookup speculation (engine.py:435-508): verify
+        steps while they pay for themselves, then the pipelined one-token graph
+        from each sequence's own position. Tokens are yielded as soon as every
+        sequence has them; a sequence that has N tokens keeps its position and
+        its verify rows are ignored."""
+        B, S, K = self.B, self.S, self.K
+        look = [NgramIndex(row) for row in input_ids]   # built while prefill runs
+        ev, ids_h = self.events, self.pin_ids
+        ev[0].synchronize()
+        first = ids_h[0].tolist()
+        yield first
+        if N == 1:
+            return
+        outs = [[t] for t in first]
+        for b in range(B):
+            look[b].extend([first[b]])
+        emitted, steps, window_base = 1, 0, 1
+        vin_h, vout_h, pos_h = self.pin_vin, self.pin_vout, self.pin_pos
+        self.spec_steps = 0
+        while emitted < N:
+            vin_h.copy_(torch.tensor([[lk.seq[-1]] + lk.draft(K) for lk in look]))
+            pos_h.copy_(torch.tensor([len(lk.seq) - 1 for lk in look], dtype=torch.int32))
+            self.vin.copy_(vin_h, non_blocking=True)
+            self.pos.copy_(pos_h, non_blocking=True)
+            self.gk.replay()
+            vout_h.copy_(self.vout, non_blocking=True)
+            ev[1].record(stream)
+            ev[1].synchronize()
+            steps += 1
+            drafts, got = vin_h.tolist(), vout_h.tolist()
+            for b in range(B):
+                if len(outs[b]) >= N:
+                    continue
+                new = accept(drafts[b], got[b])
+                outs[b].extend(new)
+                look[b].extend(new)
+            ready = min(len(o) for o in outs)
+            while emitted < min(ready, N):
+                yield [o[emitted] for o in outs]
+                emitted += 1
+            if steps % WINDOW == 0 and emitted < N:
+                advance = (ready - window_base) / WINDOW
+                window_base = ready
+                if advance < self.breakeven:
+                    break   # not paying for itself: finish on the one-token graph
+        self.spec_steps = steps
+        _log(f"B={B} S={S} N={N} K={K}: {steps} verify steps, {min(len(o) for o in outs)} "
+             f"tokens per sequence")
+        if emitted >= N:
+            return
+        # hand each sequence's last token and position to the one-token graph
+        for b in range(B):
+            ids_h[0, b] = outs[b][-1]
+            pos_h[b] = S + len(outs[b]) - 1
+        self.ids.copy_(ids_h[0], non_blocking=True)
+        self.pos.copy_(pos_h, non_blocking=True)
+        embed_ss(self.ids, self.w["embed"], self.h, None)   # the step's input rows
+        todo = N - min(len(o) for o in outs)
+        # pipelined: step j is queued before the host waits for step j-1
+        for j in range(1, todo + 1):
+            self.g1.replay()
+            ids_h[j].copy_(self.ids, non_blocking=True)
+            ev[j].record(stream)
+            if j > 1:
+                emitted = yield from self._drain(j - 1, outs, N, emitted)
+        emitted = yield from self._drain(todo, outs, N, emitted)
+
+    def _drain(self, j, outs, N, emitted):
+        self.events[j].synchronize()
+        for b, t in enumerate(self.pin_ids[j].tolist()):
+            outs[b].append(t)
+        ready = min(N, min(len(o) for o in outs))
+        while emitted < ready:
+            yield [o[emitted] for o in outs]
+            emitted += 1
+        return emitted
 
     @torch.inference_mode()
     def trace(self, input_ids: list, n: int):

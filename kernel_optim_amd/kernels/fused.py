@@ -72,7 +72,7 @@ class DecodeAttention:
     costs an L2 write-back on MI355X.
     """
 
-    MAX_T = 4
+    MAX_T = 8
 
     def __init__(self, B, T, cap, nq, nkv, d, device, target_ctas=2048, unit=None,
                  fused_combine=False):

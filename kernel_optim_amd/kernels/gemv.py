@@ -216,6 +216,17 @@ def embed_ss(ids, emb, h, ss):
               emb.shape[0], _lib.stream_ptr())
 
 
+def argmax_rows(x, ids):
+    """ids[m] = argmax_n x[m, n] over bf16 logits [M, N], lowest index on ties:
+    torch.argmax(logits, dim=-1, out=vout) of the verify step (engine.py:413-415),
+    without the memset a multi-block torch reduction records in a graph."""
+    _check(x, "x", BF16, contiguous=False)
+    _need(x.dim() == 2 and x.stride(1) == 1, "x must be [M, N] with unit column stride")
+    M, N = x.shape
+    _check(ids, "ids", torch.int64, (M,))
+    _lib.call("ko_argmax_rows", _lib.ptr(x), x.stride(0), M, N, _lib.ptr(ids), _lib.stream_ptr())
+
+
 def qk_norm_rope_acc(acc, q_w, k_w, cos, sin, pos, q_out, k_cache, v_cache, zero_buf, eps, nq,
                      nkv, d):
     """Decode (T=1) q/k norm + RoPE from the fp32 QKV accumulator (gemv.py:219-277):

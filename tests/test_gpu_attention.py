@@ -75,19 +75,25 @@ def test_ragged_small_against_oracle(dev, unit):
     torch.testing.assert_close(out.cpu().double(), want, **TOL)
 
 
-@pytest.mark.parametrize("T", [2, 3, 4])
-def test_multi_token_causal(dev, T):
+@pytest.mark.parametrize("fused_combine", [False, True])
+@pytest.mark.parametrize("T", [2, 3, 4, 5, 6, 7, 8])
+def test_multi_token_causal(dev, T, fused_combine):
+    """T query tokens per sequence, causal within the block (the verify step of
+    speculative decoding); T > 4 runs as two launches of 2-4 tokens."""
     fused = _fused()
     B, cap = 3, 200
     q, k, v = _inputs(B, T, cap, dev, seeds=(7, 8, 9))
     first = [0, 37, 200 - T]
     pos = torch.tensor(first, dtype=torch.int32, device=dev)
-    out = torch.empty_like(q)
-    att = fused.DecodeAttention(B, T, cap, 32, 8, 128, dev, unit=32)
-    att(q, k, v, pos, out)
-    torch.cuda.synchronize()
+    att = fused.DecodeAttention(B, T, cap, 32, 8, 128, dev, unit=32, fused_combine=fused_combine)
     want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [p + T for p in first], T=T)
-    torch.testing.assert_close(out.cpu().double(), want, **TOL)
+    for _ in range(2):  # the fused combine's counters re-arm between launches
+        out = torch.zeros_like(q)
+        att(q, k, v, pos, out)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().double(), want, **TOL)
+    if fused_combine:
+        assert torch.all(att.counters == 0)
 
 
 def test_config2_b16_ctx8192(dev):

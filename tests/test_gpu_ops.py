@@ -228,6 +228,46 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
         assert torch.equal(ids2, ids)
 
 
+@pytest.mark.parametrize("M,N,ld", [(5, 151936, 151936), (3, 1003, 1008), (80, 4096, 4104)])
+def test_argmax_rows_first_index_and_graph(dev, M, N, ld):
+    """ko_argmax_rows against the first-maximum argmax; planted ties (the same
+    maximum at two columns) take the lower column; rows with a stride; a tail of
+    N % 8 columns; graph replays."""
+    _, gemv = K()
+    g = _g(dev, 40)
+    buf = torch.randn(M, ld, device=dev, generator=g).to(BF)
+    x = buf[:, :N]
+    lo = torch.randint(0, N // 2, (M,), generator=torch.Generator().manual_seed(41))
+    hi = torch.randint(N // 2, N, (M,), generator=torch.Generator().manual_seed(42))
+    for m in range(M):
+        if m % 2 == 0:
+            x[m, lo[m]] = 8.0
+            x[m, hi[m]] = 8.0
+        else:
+            x[m, hi[m]] = 8.0   # the maximum alone (in the tail when N % 8 != 0)
+    want = O.argmax_first(x.cpu())
+    assert all(int(want[m]) == (lo[m] if m % 2 == 0 else hi[m]) for m in range(M))
+    ids = torch.full((M,), -1, device=dev, dtype=torch.int64)
+    gemv.argmax_rows(x, ids)
+    torch.cuda.synchronize()
+    assert torch.equal(ids.cpu(), want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gemv.argmax_rows(x, ids)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        gemv.argmax_rows(x, ids)
+    for _ in range(3):
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids.cpu(), want)
+
+
 @pytest.mark.parametrize("rows,swiglu", [(37, False), (64, True)])
 def test_tile_weights_layout(dev, rows, swiglu):
     """ko_gemv_tile against the layout written out with torch: rows padded to 16,
