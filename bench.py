@@ -46,6 +46,9 @@ def parse_args():
                     help="also measure B=16 decode (same workload at batch 16)")
     ap.add_argument("--layer", action="store_true",
                     help="also measure one fused decoder layer at B=1, 4, 16 with 2048 cached keys")
+    ap.add_argument("--spec", action="store_true",
+                    help="also measure B=1 decode with prompt-lookup speculation (the same "
+                         "random prompt, and a prompt of a repeated 64-token pattern)")
     return ap.parse_args()
 
 
@@ -142,6 +145,42 @@ def bench_decode(args, eng=None, B=1):
     }
     if not args.no_cpu and B == 1:
         res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
+    return res
+
+
+def bench_spec(args, eng, B=1):
+    """Greedy decode with prompt-lookup speculation (Engine(spec=True)), same
+    model and sizes as bench_decode, two prompts: seeded uniform-random ids (the
+    decode workload: lookup rarely matches, so the engine falls back to the
+    one-token graph after its first acceptance check) and a 64-token seeded
+    pattern repeated to the prompt length (lookup matches). tok/s counts the
+    tokens after the first over all sequences; the verify-step and one-token
+    step times are the engine's own graph timings at setup."""
+    import torch
+    cfg = eng.cfg
+    S, N = args.prompt, args.new_tokens
+    g = torch.Generator().manual_seed(0)
+    prompts = {
+        "random": torch.randint(0, cfg.vocab, (B, S), generator=g).tolist(),
+        "repeated_pattern": torch.randint(0, cfg.vocab, (B, 64), generator=g)
+                                 .repeat(1, -(-S // 64))[:, :S].tolist(),
+    }
+    res = {"workload": f"Qwen3-4B architecture greedy decode with prompt-lookup speculation, "
+                       f"B={B}, prompt {S}, {N} new tokens, random-init bf16 weights (seed 0)"}
+    for name, prompt in prompts.items():
+        for _ in eng.generate(prompt, N):      # setup, tuning, capture, warm-up
+            pass
+        torch.cuda.synchronize()
+        t0 = None
+        for i, _ in enumerate(eng.generate(prompt, N)):
+            if i == 0:
+                t0 = time.perf_counter()
+        el = time.perf_counter() - t0
+        res[name] = {"tok_s": round(B * (N - 1) / el, 2), "verify_steps": eng.spec_steps}
+    res.update({"K": eng.K, "verify_rows": B * (eng.K + 1),
+                "verify_path": "fused GEMV" if eng.verify_fused else "hipBLASLt",
+                "t_step_ms": round(eng.t_step_ms, 4), "t_verify_ms": round(eng.t_verify_ms, 4),
+                "breakeven_tokens_per_verify": round(eng.breakeven, 3)})
     return res
 
 
@@ -416,6 +455,12 @@ def main():
         line["decode_b1"] = bench_decode(args, eng, B=1)
         if args.decode_b16:
             line["decode_b16"] = bench_decode(args, eng, B=16)
+        del eng
+        torch.cuda.empty_cache()
+    if args.spec:
+        from kernel_optim_amd.engine import Engine
+        eng = Engine("random", spec=True)
+        line["decode_b1_spec"] = bench_spec(args, eng, B=1)
         del eng
         torch.cuda.empty_cache()
     if not args.no_attn and not args.no_ragged:

@@ -361,6 +361,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (int e = 0; e < 8; ++e) {
           acc[t][j][e] = sum_xor32(sum_xor16(acc[t][j][e]));
         }
+    // With FUSED the partials are read back in this launch by another
+    // workgroup: device-coherent stores (no L2 write-back needed).
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const long long R = (long long)(b * a.tstride + a.t0 + t) * nq + kvh * G + g;
@@ -368,10 +370,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         if (g == j) {
-          reinterpret_cast<float4*>(dst)[0] =
-              make_float4(acc[t][j][0], acc[t][j][1], acc[t][j][2], acc[t][j][3]);
-          reinterpret_cast<float4*>(dst)[1] =
-              make_float4(acc[t][j][4], acc[t][j][5], acc[t][j][6], acc[t][j][7]);
+          if constexpr (FUSED) {
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+              store_coherent(dst + e, make_float2(acc[t][j][e], acc[t][j][e + 1]));
+          } else {
+            reinterpret_cast<float4*>(dst)[0] =
+                make_float4(acc[t][j][0], acc[t][j][1], acc[t][j][2], acc[t][j][3]);
+            reinterpret_cast<float4*>(dst)[1] =
+                make_float4(acc[t][j][4], acc[t][j][5], acc[t][j][6], acc[t][j][7]);
+          }
         }
       }
     }
@@ -385,26 +393,30 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
           l = (r == j) ? lrow[j] : l;
         }
       const long long R = (long long)(b * a.tstride + a.t0 + g) * nq + kvh * G + r;
-      reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(m, l);
+      if constexpr (FUSED)
+        store_coherent(a.ml + 2 * (R * max_units + c), make_float2(m, l));
+      else
+        reinterpret_cast<float2*>(a.ml)[R * max_units + c] = make_float2(m, l);
     }
 
     if constexpr (FUSED) {
-      // Publish this unit's partials, count its arrival; the last arrival of
-      // the (b, kv_head) pair merges the pair's partials.
-      __threadfence();
+      // Count the unit's arrival once this wavefront's partial stores are
+      // performed at device scope; the last arrival of the (b, kv_head) pair
+      // merges the pair's partials with device-scope loads.
+      __builtin_amdgcn_s_waitcnt(0);
       int prev = 0;
       int* ctr = a.counters + (long long)b * nkv + kvh;
-      if (lane == 0) prev = atomicAdd(ctr, 1);
+      if (lane == 0) prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       prev = readlane(prev, 0);
       const int n = nunits(kv_len, unit);
       if (prev == n - 1) {
-        __threadfence();
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
           for (int j = 0; j < G; ++j)
-            combine_row<32>(a.o_part, a.ml, (long long)(b * a.tstride + a.t0 + t) * nq + kvh * G + j,
-                            n, nullptr, 0, a.cap, unit, max_units, a.out);
+            combine_row<32, true>(a.o_part, a.ml,
+                                  (long long)(b * a.tstride + a.t0 + t) * nq + kvh * G + j, n,
+                                  nullptr, 0, a.cap, unit, max_units, a.out);
         if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }

@@ -267,8 +267,9 @@ class Engine:
         self.qT = torch.zeros(M, cfg.nq * cfg.head_dim, dtype=bf, device=dev)
         self.attT = torch.zeros_like(self.qT)
         self.actT = torch.zeros(M, cfg.inter, dtype=bf, device=dev)
-        self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
-                                     fused_combine=True)
+        # the merge as its own launch: one wavefront per row, where the fused
+        # combine would merge a pair's T x 4 rows in one wavefront
+        self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
         self.verify_fused = M <= FUSED_VERIFY_ROWS
         if self.verify_fused:   # one weight pass per projection on the fused GEMVs
             self.gvk = dict(
