@@ -193,7 +193,8 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     are captured in one graph and timed with events."""
     import torch
     from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
-    from kernel_optim_amd.kernels.gemv import EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, tile_weights
+    from kernel_optim_amd.kernels.gemv import (EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, tile_weights,
+                                               uses_tiled)
     from kernel_optim_amd.engine import _rope_tables
     from kernel_optim_amd.model import Qwen3Config, random_weights
     cfg = Qwen3Config(layers=nsets)
@@ -228,10 +229,10 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         for name in ("qkv", "o", "gu", "down"):
             raw = [l[name] for l in L]
             tiled = None
-            if any(c[0] == 2 for c in ops[name].candidates()):
+            if any(uses_tiled(c) for c in ops[name].candidates()):
                 tiled = tiles.setdefault(name, [tile_weights(w_, swiglu=name == "gu") for w_ in raw])
             ops[name].tune(raw, time.monotonic() + 20, tiled=tiled)
-            W[name] = tiled if ops[name].cfg[0] == 2 else raw
+            W[name] = tiled if uses_tiled(ops[name].cfg) else raw
 
         def layer(i):
             lw = L[i]

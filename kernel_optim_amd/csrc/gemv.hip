@@ -511,6 +511,139 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   }
 }
 
+// layout 3: the layout-2 weight tiles with the K range of a tile cut into
+// slices, one 4-wavefront workgroup per (tile, slice), a grid of
+// ntiles * slices workgroups (not persistent). Wavefront w of slice q takes the
+// S consecutive 32-wide K steps starting at (4 q + w) S, so slices = K / (128 S).
+// With one slice the workgroup runs the epilogue itself. With more, each writes
+// its fp32 16 x 16 partial tile to its own slot with device-coherent stores and
+// counts its arrival on the tile's counter; the last to arrive adds the slots
+// in slice order (the result does not depend on the arrival order), re-arms
+// the counter and runs the epilogue. NORM computes the row norms from the
+// wavefronts' x slices, so it needs one slice (or ss given).
+constexpr int KSW = 4;       // wavefronts per workgroup of layout 3
+constexpr int KS_MAX = 32;   // slices per tile
+template <int EPI, bool NORM, int S, int PD>
+__global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int* __restrict__ ctr,
+                                                               float* __restrict__ slots) {
+  static_assert(EPI != EPI_ARGMAX, "the split-K layout has no argmax epilogue");
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
+  __shared__ float s_c[KSW][NW][16][17];
+  __shared__ float s_sq[KSW][16];
+  __shared__ int s_prev;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, mr = a.mrows;
+  const int nsl = K / (32 * S * KSW);
+  const int tile = blockIdx.x / nsl, slice = blockIdx.x - tile * nsl;
+  const int T = (N + 15) / 16, KS = K / 32;
+  const int sb = (slice * KSW + wv) * S;  // this wavefront's first K step
+  const int kw0 = sb * 32 + 8 * g;        // this lane's first k
+  const bool mok = col < mr;
+
+  const uint16_t* wlane = a.w + 8 * lane;
+  uint4 wb[PD][NW];
+  auto issue = [&](int s, int slot) {
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + sb + s) * 512);
+  };
+#pragma unroll
+  for (int s = 0; s < PD; ++s) issue(s, s);  // weights do not depend on x
+
+  bf16x8 xa[S];
+  {
+    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+    uint4 xr[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM) {
+      float rstd;
+      if (a.ss) {
+        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+      } else {  // one slice: the KSW wavefronts hold the whole row
+        float sq = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) sq += sq8(xr[s]);
+        sq = sum_xor32(sum_xor16(sq));
+        if (g == 0) s_sq[wv][col] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < KSW; ++w) tot += s_sq[w][col];
+        rstd = rsqrtf(tot / (float)K + a.eps);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], ldg16(a.nw + kw0 + 32 * s), rstd);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
+  }
+
+  f32x4 c[NW];
+#pragma unroll
+  for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int slot = s % PD;
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
+                                                     c[r], 0, 0, 0);
+    if (s + PD < S) issue(s + PD, slot);
+  }
+  // C lane layout: column col, rows 4g + i.
+#pragma unroll
+  for (int r = 0; r < NW; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_c[wv][r][4 * g + i][col] = c[r][i];
+  __syncthreads();
+  const int m = t >> 4, j = t & 15, n = tile * 16 + j;
+  float tot = 0.f, tot2 = 0.f;
+#pragma unroll
+  for (int w = 0; w < KSW; ++w) {
+    tot += s_c[w][0][m][j];
+    if constexpr (NW == 2) tot2 += s_c[w][NW - 1][m][j];
+  }
+  if (nsl > 1) {
+    float* mine = slots + ((long long)(tile * nsl + slice) * NW) * 256 + t;
+    __hip_atomic_store(mine, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (NW == 2) __hip_atomic_store(mine + 256, tot2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's slot stores are performed
+    __syncthreads();
+    if (t == 0) s_prev = __hip_atomic_fetch_add(ctr + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_prev != nsl - 1) return;
+    const float* base = slots + (long long)tile * nsl * NW * 256 + t;
+    float v[KS_MAX], v2[KS_MAX];
+#pragma unroll
+    for (int q = 0; q < KS_MAX; ++q) {
+      v[q] = q < nsl ? __hip_atomic_load(base + q * NW * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      if constexpr (NW == 2)
+        v2[q] = q < nsl ? __hip_atomic_load(base + q * NW * 256 + 256, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+    tot = 0.f;
+    tot2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < KS_MAX; ++q) {
+      if (q < nsl) {
+        tot += v[q];
+        if constexpr (NW == 2) tot2 += v2[q];
+      }
+    }
+    if (t == 0) __hip_atomic_store(ctr + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool ok = m < mr && n < N;
+  float h2 = 0.f;
+  if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+  if constexpr (EPI == EPI_RESID) {
+    if (a.ss_out) {
+      h2 = row_sum16(h2);
+      if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+    }
+  }
+}
+
 // Weight layout of layout 2 ("tiled"): rows padded to a multiple of 16; for
 // row tile t and k step s (32 columns) a 1 KiB block at ((t * K/32 + s) * 64 + l)
 // * 8 elements holds, for lane l, row 16 t + l % 16, columns 32 s + 8 (l / 16)
@@ -821,11 +954,69 @@ int launch_mfma(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s
   }
 }
 
+// Steps per wavefront of layout 3 for K and a slice count (0: unsupported):
+// S in {20, 19, 8, 4} with K = 128 * S * slices.
+int ks_steps(int K, int slices) {
+  if (slices < 1 || slices > KS_MAX || K % (128 * slices)) return 0;
+  const int S = K / (128 * slices);
+  return (S == 20 || S == 19 || S == 8 || S == 4) ? S : 0;
+}
+
+template <int S, int PD>
+int launch_mfma_ks_s(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                     hipStream_t s) {
+  const int grid = ((a.N + 15) / 16) * slices;
+#define KO_K(NORMV, EPIV)                                                                  \
+  hipLaunchKernelGGL((gemv_mfma_ks_kernel<EPIV, NORMV, S, PD>), dim3(grid), dim3(64 * KSW), 0, s, \
+                     a, ctr, slots)
+  if (norm) {
+    if constexpr (S == 20) {
+      switch (epi) {
+        case EPI_F32: KO_K(true, EPI_F32); break;
+        case EPI_BF16: KO_K(true, EPI_BF16); break;
+        case EPI_RESID: KO_K(true, EPI_RESID); break;
+        default: KO_K(true, EPI_SWIGLU); break;
+      }
+    } else {
+      return KO_ENOTSUP;
+    }
+  } else {
+    switch (epi) {
+      case EPI_F32: KO_K(false, EPI_F32); break;
+      case EPI_BF16: KO_K(false, EPI_BF16); break;
+      case EPI_RESID: KO_K(false, EPI_RESID); break;
+      default: KO_K(false, EPI_SWIGLU); break;
+    }
+  }
+#undef KO_K
+  return KO_LAUNCH_STATUS();
+}
+
+int launch_mfma_ks(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                   hipStream_t s) {
+  switch (ks_steps(a.K, slices)) {
+    case 20: return launch_mfma_ks_s<20, 10>(a, epi, norm, slices, ctr, slots, s);
+    case 19: return launch_mfma_ks_s<19, 10>(a, epi, norm, slices, ctr, slots, s);
+    case 8: return launch_mfma_ks_s<8, 8>(a, epi, norm, slices, ctr, slots, s);
+    case 4: return launch_mfma_ks_s<4, 4>(a, epi, norm, slices, ctr, slots, s);
+    default: return KO_ENOTSUP;
+  }
+}
+
+// Layout 3 scratch (fp32 elements): the tiles' arrival counters (int32, zero
+// before the first launch, left at zero by every launch), padded to 64, then
+// two 16 x 16 fp32 slots (gate and up) per (tile, slice).
+long long ks_scratch(int N, int slices) {
+  const long long T = (N + 15) / 16;
+  return ((T + 63) / 64) * 64 + T * slices * 2 * 256;
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 long long parts_for(int N, int layout, int rows, int waves) {
   if (layout == 0) return (N + rows - 1) / rows;
   if (layout == 2) return mfma_grid(N, rows);
+  if (layout != 1 || waves < 1) return 0;  // layout 3 has no ARGMAX partials
   const long long units = (N + rows - 1) / rows;
   return ((units + waves - 1) / waves) * waves;
 }
@@ -847,11 +1038,17 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
   if (layout == 0) {
     if (rows != 4 && rows != 8 && !(rows == 16 && M <= 2)) return KO_ENOTSUP;
   } else if (layout == 1) {
+    if (waves != 2 && waves != 4) return KO_ENOTSUP;
     if (M > 4) return KO_ENOTSUP;
     if (norm && (long long)M * K * 2 > LDS_X_BYTES) return KO_ENOTSUP;
   } else if (layout == 2) {
     if (rows != 1 && rows != 2 && rows != 4) return KO_ENOTSUP;
     if (!mfma_supported(K, epi)) return KO_ENOTSUP;
+  } else if (layout == 3) {
+    if (epi == EPI_ARGMAX || !ks_steps(K, rows)) return KO_ENOTSUP;
+    if (norm && rows > 1 && !ss) return KO_ENOTSUP;
+    if (norm && ks_steps(K, rows) != 20) return KO_ENOTSUP;
+    if (rows > 1 && (!part || !al16(part) || part_len < ks_scratch(N, rows))) return KO_ERANGE;
   } else {
     return KO_EINVAL;
   }
@@ -892,8 +1089,11 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
                        : launch_block_r16(a, epi, norm != 0, s);
     else if (layout == 1)
       st = launch_wave_cfg(a, epi, norm != 0, rows, waves, s);
-    else
+    else if (layout == 2)
       st = launch_mfma(a, epi, norm != 0, rows, s);
+    else
+      st = launch_mfma_ks(a, epi, norm != 0, rows, reinterpret_cast<int*>(part),
+                          part + ((N + 15) / 16 + 63) / 64 * 64, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
       hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(FT), 0, s, a.part, a.nparts,
@@ -930,7 +1130,8 @@ int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, vo
 // fp32 scratch elements ko_gemv needs for EPI 4 (ARGMAX) with this layout
 // (a size, not a status; -1 for bad arguments).
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
-  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 2) return -1;
+  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 3) return -1;
+  if (layout == 3) return rows > 1 ? ks_scratch(N, rows) : 0;
   return 2LL * 16 * parts_for(N, layout, rows, waves);
 }
 

@@ -43,7 +43,7 @@ import torch
 
 from .kernels.fused import DecodeAttention, add_rms_norm, qk_norm_rope, rope_rows, silu_mul
 from .kernels.gemv import (EPI_ARGMAX, EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, argmax_rows,
-                           embed_ss, tile_weights)
+                           embed_ss, tile_weights, uses_tiled)
 from .model import Qwen3Config, load_checkpoint, random_weights
 from .prefill import prefill
 
@@ -237,12 +237,12 @@ class Engine:
         self.gw = {}
         for name, g in self.gv.items():
             tiled = None
-            if any(c[0] == 2 for c in g.candidates()):
+            if any(uses_tiled(c) for c in g.candidates()):
                 tiled = self._tiled(name, raw[name])
             if TUNE:
                 g.tune(raw[name], deadline, tiled=tiled)
                 _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
-            self.gw[name] = tiled if g.cfg[0] == 2 else raw[name]
+            self.gw[name] = tiled if uses_tiled(g.cfg) else raw[name]
         self.g1 = self._capture(self._step1)
         self.gk = None
         if self.K:
@@ -282,12 +282,12 @@ class Engine:
             self.gwk = {}
             for name, g in self.gvk.items():
                 tiled = None
-                if any(c[0] == 2 for c in g.candidates()):
+                if any(uses_tiled(c) for c in g.candidates()):
                     tiled = self._tiled(name, raw[name])
                 if TUNE:
                     g.tune(raw[name], deadline, tiled=tiled)
                     _log(f"verify gemv {name} M={M} cfg={g.cfg} {g.us:.1f}us")
-                self.gwk[name] = tiled if g.cfg[0] == 2 else raw[name]
+                self.gwk[name] = tiled if uses_tiled(g.cfg) else raw[name]
         else:                   # hipBLASLt GEMMs between the fused ops
             self.nT = torch.zeros(M, H, dtype=bf, device=dev)
             self.guT = torch.zeros(M, 2 * cfg.inter, dtype=bf, device=dev)

@@ -34,6 +34,11 @@ from .fused import BF16, _cdiv, _check, _need
 EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3, 4
 
 
+def uses_tiled(cfg):
+    """Layouts 2 and 3 (MFMA) read the tile_weights copy of the weights."""
+    return cfg[0] in (2, 3)
+
+
 class Gemv:
     """One fused projection y[M, N] = x[M, K] @ W[N, K]^T with a norm prologue and
     an epilogue; its launch config is picked by GPU timing at setup."""
@@ -52,6 +57,18 @@ class Gemv:
         SWIGLU only up to 4096 (gemv.hip, mfma_supported)."""
         return self.K in (2560, 4096) or (self.K == 9728 and self.epi != EPI_SWIGLU)
 
+    def ks_slices(self):
+        """K slices layout 3 takes for this projection (gemv.hip, ks_steps):
+        K = 128 * S * slices with S in {20, 19, 8, 4}; NORM computes the row norms
+        in one workgroup, so it takes one slice (K = 2560); no ARGMAX."""
+        if self.epi == EPI_ARGMAX:
+            return []
+        out = []
+        for s in (1, 2, 4, 8, 19):
+            if self.K % (128 * s) == 0 and self.K // (128 * s) in (20, 19, 8, 4):
+                out.append(s)
+        return [s for s in out if s == 1 and self.K == 2560] if self.norm else out
+
     def candidates(self):
         """Launch configurations, the default first. Layout 1 (a wavefront per row
         group) is the batch-1..4 path; layout 0 serves every batch up to 16 rows
@@ -59,6 +76,7 @@ class Gemv:
         (``(2, per_cu, 0)``: a persistent grid of 256 x per_cu workgroups)."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
+        mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
         if self.M > 4:
             out += mfma
             mfma = []
@@ -73,9 +91,12 @@ class Gemv:
         return out + mfma
 
     def _scratch(self, device, cfg):
+        """fp32 scratch of the ARGMAX partials or of layout 3's slots and arrival
+        counters (allocated zeroed: the counters start at zero and every launch
+        leaves them there)."""
         n = _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg)
         if self._part is None or self._part.device != device or self._part.numel() < n:
-            self._part = torch.empty(max(n, 2), dtype=torch.float32, device=device)
+            self._part = torch.zeros(max(n, 2), dtype=torch.float32, device=device)
         return self._part
 
     def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None,
@@ -86,7 +107,7 @@ class Gemv:
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
-        nrows = _cdiv(N, 16) * 16 if layout == 2 else N  # layout 2: tile_weights copy
+        nrows = _cdiv(N, 16) * 16 if uses_tiled((layout,)) else N  # the tile_weights copy
         _check(w, "w", BF16, ((2 * nrows) if epi == EPI_SWIGLU else nrows, K))
         if self.norm:
             _check(nw, "nw", BF16, (K,))
@@ -110,7 +131,8 @@ class Gemv:
             if next_emb is not None:
                 _check(next_emb, "next_emb", BF16, (N, K))
                 _check(next_h, "next_h", BF16, (M, K))
-        part = self._scratch(x.device, (layout, rows, waves)) if epi == EPI_ARGMAX else None
+        part = (self._scratch(x.device, (layout, rows, waves))
+                if epi == EPI_ARGMAX or (layout == 3 and rows > 1) else None)
         _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
                   _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
                   _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(pos_inc),
@@ -134,17 +156,17 @@ class Gemv:
         h = torch.zeros(M, N, device=dev, dtype=BF16)
         ids = torch.zeros(M, device=dev, dtype=torch.int64)
         kw = dict(y=y, nw=nw, h=h, ids=ids)
-        if self.epi == EPI_ARGMAX:
-            # the scratch is sized for every candidate before any graph captures
-            # it: the graphs are replayed after all captures
-            for cfg in self.candidates():
-                if _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg) > 0:
-                    self._scratch(dev, cfg)
+        # the scratch is sized for every candidate before any graph captures it:
+        # the graphs are replayed after all captures
+        for cfg in self.candidates():
+            if ((self.epi == EPI_ARGMAX or cfg[0] == 3)
+                    and _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg) > 0):
+                self._scratch(dev, cfg)
         graphs = []
         for cfg in self.candidates():
             if time.monotonic() > deadline:
                 break
-            ws = tiled if cfg[0] == 2 else weights
+            ws = tiled if uses_tiled(cfg) else weights
             if ws is None:
                 continue
             try:

@@ -71,3 +71,29 @@ def test_wrapper_raises_runtime_error_on_status():
     with pytest.raises(RuntimeError):
         _lib.call("ko_decode_attn_partial", None, None, None, None, 1, 64, 0, 0, 1, 1, 8, 128,
                   64, 1, 1, 0.1, None, None, None)
+
+
+def test_gemv_host_path_of_every_layout_without_gpu(libpath):
+    """ko_gemv's host logic for every layout runs to the launch without a fault
+    (layout 3 once divided by the layout-1 wave count, zero there); with no GPU
+    the launch itself reports a HIP status. Bad layout-1 wave counts are refused
+    first. Skipped where a GPU is visible: the pointers are fake."""
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("fake pointers must not reach a real launch")
+    from kernel_optim_amd import _lib
+    h = _lib.lib()
+    P = 1 << 20
+    for K, layout, rows, waves in [(4096, 3, 4, 0), (4096, 3, 8, 0), (9728, 3, 4, 0),
+                                   (9728, 3, 19, 0), (2560, 3, 1, 0), (2560, 2, 1, 0),
+                                   (2560, 0, 8, 0)]:
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 2, 2560, K,
+                       1, 0, 0, layout, rows, waves, 1e-6, None)
+        assert st > 0, (K, layout, rows, st)   # a HIP status from the launch, not a host error
+    for waves in (0, 1, 3):
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 2, 2560,
+                       2560, 1, 0, 0, 1, 2, waves, 1e-6, None)
+        assert st == -95
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 16, 2, 2560, 4096, 1, 0,
+                   0, 3, 4, 0, 1e-6, None)
+    assert st == -34   # layout 3 scratch too small

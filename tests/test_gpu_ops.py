@@ -182,6 +182,90 @@ def test_gemv_epilogues(dev, M, cfg):
     assert_bf16_close(y.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
 
 
+@pytest.mark.parametrize("M", [2, 7, 16, 20])
+def test_gemv_split_k_layout(dev, M):
+    """Layout 3 (MFMA tiles, K cut into slices merged by the last workgroup of
+    each tile, in slice order) for every Qwen3-4B projection and every slice
+    count it takes, against the oracle; bit-identical on a second call and on
+    graph replays (the arrival counters re-arm); M = 20 runs as 16 + 4 rows on
+    the same counters."""
+    _, gemv = K()
+    g = _g(dev, 50 + M)
+    nw = (1 + 0.1 * torch.randn(2560, device=dev, generator=g)).to(BF)
+    cases = []
+    # qkv: NORM + BF16 (one slice: the row norm needs the whole row)
+    N, Kd = SHAPES["qkv"]
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 60)
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_BF16, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+    cases.append(("qkv", gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=True), x,
+                  gemv.tile_weights(W), dict(nw=nw), "y", N, want))
+    # gu: NORM + SWIGLU
+    N, Kd = SHAPES["gu"]
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 61, rows=2 * N)
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_SWIGLU, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+    cases.append(("gu", gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True), x,
+                  gemv.tile_weights(W, swiglu=True), dict(nw=nw), "y", N, want))
+    # o: RESID; down: BF16
+    for name, epi, seed in (("o", gemv.EPI_RESID, 62), ("down", gemv.EPI_BF16, 63)):
+        N, Kd = SHAPES[name]
+        a = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+        W = _weights(dev, N, Kd, seed)
+        h0 = torch.randn(M, N, device=dev, generator=g).to(BF)
+        if epi == gemv.EPI_RESID:
+            want, _ = O.gemv(a.cpu(), W.cpu(), O.EPI_RESID, h=h0.cpu())
+        else:
+            want = O.gemv(a.cpu(), W.cpu(), O.EPI_BF16)
+        cases.append((name, gemv.Gemv(M, N, Kd, epi, norm=False), a, gemv.tile_weights(W),
+                      dict(h0=h0), "h" if epi == gemv.EPI_RESID else "y", N, want))
+    seen = set()
+    for name, op, xin, Wt, extra, out_name, N, want in cases:
+        slices = op.ks_slices()
+        assert slices, f"{name}: layout 3 offers no slice count"
+        for sl in slices:
+            seen.add((name, sl))
+            cfg = (3, sl, 0)
+
+            def run():
+                kw = {}
+                if "nw" in extra:
+                    kw["nw"] = extra["nw"]
+                if out_name == "h":
+                    kw["h"] = extra["h0"].clone()
+                    res = kw["h"]
+                else:
+                    kw["y"] = torch.empty(M, N, device=dev, dtype=BF)
+                    res = kw["y"]
+                op(xin, Wt, cfg=cfg, **kw)
+                return res, kw
+
+            r1, _ = run()
+            torch.cuda.synchronize()
+            assert_bf16_close(r1.cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
+            r2, _ = run()
+            torch.cuda.synchronize()
+            assert torch.equal(r1, r2), f"{name} slices {sl}: not deterministic"
+            # graph replays against the eager result
+            s_ = torch.cuda.Stream()
+            s_.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s_):
+                run()
+            torch.cuda.current_stream().wait_stream(s_)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                r3, kw3 = run()
+            for _ in range(3):
+                if out_name == "h":
+                    kw3["h"].copy_(extra["h0"])
+                torch.cuda.synchronize()
+                gr.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(r3, r1), f"{name} slices {sl}: graph replay differs"
+    assert {("o", 4), ("o", 8), ("down", 4), ("down", 19), ("qkv", 1), ("gu", 1)} <= seen
+
+
 @pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (16, (0, 8, 0)),
                                    (3, (2, 1, 0)), (16, (2, 2, 0))])
 def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
