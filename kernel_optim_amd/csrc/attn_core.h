@@ -140,7 +140,9 @@ __device__ void combine_row(const float* __restrict__ o_part, const float* __res
   float L = 0.f, o0 = 0.f, o1 = 0.f, M = NEG_BIG;
   static_assert(NB <= 64, "one (m, l) slot per lane");
   for (int c0 = 0; c0 < max_units; c0 += NB) {
-    const int cn = min(NB, max_units - c0);
+    // slots to load: the valid ones when n is known, else every slot (n is
+    // read from the lengths while the loads are in flight)
+    const int cn = n >= 0 ? min(NB, max(0, n - c0)) : min(NB, max_units - c0);
     const float2 mlc = lane < cn ? load2<COHERENT>(mlr + 2 * (c0 + lane)) : make_float2(NEG_BIG, 0.f);
     float2 a[NB];
 #pragma unroll
