@@ -415,18 +415,26 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
     for (int r = 0; r < NW; ++r)
       wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + s) * 512);
   };
-  // The first tile's weights do not depend on x: issue them before the prologue.
-#pragma unroll
-  for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
-
   // This wavefront's K slice of x (A operand, row m = col), kept in registers
-  // for every tile; NORM normalises it once.
+  // for every tile; NORM normalises it once. x (and, where registers allow, the
+  // NORM gain) is loaded first, then the first tile's weights: loads return in
+  // issue order, so the prologue runs while the weights stream. The weights
+  // stay issued there (the scheduler would otherwise sink the loads next to
+  // their MFMAs to save registers).
+  constexpr bool NW_EARLY = NORM && S <= 10;
   bf16x8 xa[S];
   {
     const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
-    uint4 xr[S];
+    uint4 xr[S], nwv[NW_EARLY ? S : 1];
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NW_EARLY) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) {
       float rstd;
       if (a.ss) {
@@ -444,7 +452,12 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
         rstd = rsqrtf(tot / (float)K + a.eps);
       }
 #pragma unroll
-      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], ldg16(a.nw + kw0 + 32 * s), rstd);
+      for (int s = 0; s < S; ++s) {
+        uint4 w;
+        if constexpr (NW_EARLY) w = nwv[s];
+        else w = ldg16(a.nw + kw0 + 32 * s);
+        xr[s] = norm8(xr[s], w, rstd);
+      }
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
@@ -547,15 +560,24 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
     for (int r = 0; r < NW; ++r)
       wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + sb + s) * 512);
   };
-#pragma unroll
-  for (int s = 0; s < PD; ++s) issue(s, s);  // weights do not depend on x
 
+  // x (and the NORM gain) first: loads return in issue order, so the prologue
+  // then runs while the weights stream instead of after them.
   bf16x8 xa[S];
   {
     const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
-    uint4 xr[S];
+    uint4 xr[S], nwv[NORM ? S : 1];
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < PD; ++s) issue(s, s);
+    // keep the whole ring issued here: the scheduler would otherwise sink the
+    // weight loads next to their MFMAs to save registers, leaving ~3 in flight
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) {
       float rstd;
       if (a.ss) {
@@ -573,7 +595,7 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
         rstd = rsqrtf(tot / (float)K + a.eps);
       }
 #pragma unroll
-      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], ldg16(a.nw + kw0 + 32 * s), rstd);
+      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], nwv[s], rstd);
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
@@ -994,9 +1016,15 @@ int launch_mfma_ks_s(const GemvArgs& a, int epi, bool norm, int slices, int* ctr
 
 int launch_mfma_ks(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s) {
+  // every weight step in flight at once, except SWIGLU's two tiles at 20 steps
+  // (registers)
   switch (ks_steps(a.K, slices)) {
-    case 20: return launch_mfma_ks_s<20, 10>(a, epi, norm, slices, ctr, slots, s);
-    case 19: return launch_mfma_ks_s<19, 10>(a, epi, norm, slices, ctr, slots, s);
+    case 20:
+      if (epi == EPI_SWIGLU) return launch_mfma_ks_s<20, 10>(a, epi, norm, slices, ctr, slots, s);
+      return launch_mfma_ks_s<20, 20>(a, epi, norm, slices, ctr, slots, s);
+    case 19:
+      if (epi == EPI_SWIGLU) return launch_mfma_ks_s<19, 10>(a, epi, norm, slices, ctr, slots, s);
+      return launch_mfma_ks_s<19, 19>(a, epi, norm, slices, ctr, slots, s);
     case 8: return launch_mfma_ks_s<8, 8>(a, epi, norm, slices, ctr, slots, s);
     case 4: return launch_mfma_ks_s<4, 4>(a, epi, norm, slices, ctr, slots, s);
     default: return KO_ENOTSUP;
