@@ -324,12 +324,16 @@ def bench_attention(args):
           for i in range(nbuf)]
     pos = torch.full((B,), CTX - 1, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
+    # the reference's two-launch form (partials, then a combine launch)
     att = DecodeAttention(B, 1, CTX, NQ, NKV, D, dev)
+    # the form the engine runs: partials and the LSE merge in one launch
+    att2 = DecodeAttention(B, 1, CTX, NQ, NKV, D, dev, fused_combine=True)
     print(f"[bench] attention B={B} ctx={CTX} unit={att.unit} units={att.max_units * B * NKV} "
           f"grid_waves={att.grid_waves}", file=sys.stderr, flush=True)
 
     for i in range(args.warmup):
         att(q, ks[i % nbuf], vs[i % nbuf], pos, out)
+        att2(q, ks[i % nbuf], vs[i % nbuf], pos, out)
     torch.cuda.synchronize()
 
     # ---- timed region: K steps, synchronised on both sides ----
@@ -361,6 +365,14 @@ def bench_attention(args):
     torch.cuda.synchronize()
     k_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     k_gbs = nbytes / (k_ms * 1e-3) / 1e9
+
+    # ---- the one-launch form (the merge by the last unit of each pair) ----
+    e0.record()
+    for i in range(args.steps):
+        att2(q, ks[i % nbuf], vs[i % nbuf], pos, out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms2 = e0.elapsed_time(e1) / args.steps
     del ks, vs
 
     # ---- measured copy bandwidth for reference ----
@@ -392,6 +404,9 @@ def bench_attention(args):
                      "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
                      "avg_kernel_us": round(k_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": nbytes},
+        "one_launch": {"gbs": round(nbytes / (ms2 * 1e-3) / 1e9, 2), "ms_per_op": round(ms2, 5),
+                       "form": "partials and the LSE merge in one launch (fused_combine=True, "
+                               "as the engine runs it)"},
         "measured_copy_gbs": round(copy_gbs, 1),
     }
 

@@ -112,6 +112,15 @@ def test_config2_b16_ctx8192(dev):
     sel = [0, 5, 10, 15]
     want = A.decode_attention(q.view(B, -1)[sel].cpu(), k[sel].cpu(), v[sel].cpu(), [cap] * 4)
     torch.testing.assert_close(out.view(B, -1)[sel].cpu().double(), want, **TOL)
+    # the same op with the merge in the partial launch (as the engine and the
+    # benchmark run it): bit-identical, on repeated launches
+    attf = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev, fused_combine=True)
+    for _ in range(3):
+        outf = torch.zeros_like(q)
+        attf(q, k, v, pos, outf)
+        torch.cuda.synchronize()
+        assert torch.equal(outf, out)
+    assert torch.all(attf.counters == 0)
 
 
 def test_config3_ragged_padded_tail_unread(dev):
