@@ -189,15 +189,25 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           grid of 256 * `rows` (1, 2 or 4) workgroups. w must be in the tiled
  *           layout written by ko_gemv_tile (for SWIGLU: the gate rows tiled,
  *           then the up rows tiled, each padded to a multiple of 16 rows).
+ * layout 3: layout 2's tiles and weight copy with the K range of a tile cut
+ *           into `rows` slices (K = 128 * S * rows, S in {20, 19, 8, 4}), one
+ *           4-wavefront workgroup per (tile, slice); the last slice of a tile
+ *           to arrive adds the slices' fp32 partial tiles in slice order
+ *           (deterministic) and runs the epilogue. No ARGMAX; NORM only with
+ *           S = 20 and, for rows > 1, ss given. For rows > 1, part is its
+ *           scratch (part_len >= ko_gemv_argmax_scratch(N, 3, rows, 0)): zero
+ *           before the first call, left zero by every call (the tiles' arrival
+ *           counters); calls that share it must not overlap.
  * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
             float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
             float* part, long long part_len, int M, int N, int K, int epi, int norm,
             int accumulate, int layout, int rows, int waves, float eps, void* stream);
 
-/* Number of fp32 scratch elements epi 4 (ARGMAX) needs for N columns with this
- * launch configuration (a size, not a status; -1 for bad arguments). Helper of
- * ko_gemv, no reference counterpart. */
+/* Number of fp32 scratch elements ko_gemv needs for N columns with this launch
+ * configuration: the ARGMAX partials (epi 4) of layouts 0-2, or layout 3's
+ * slots and counters (rows > 1). A size, not a status; -1 for bad arguments.
+ * Helper of ko_gemv, no reference counterpart. */
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
 
 /* Replaces torch.argmax(logits, dim=-1, out=vout) of the speculative verify
