@@ -6,8 +6,9 @@ engine/engine.py) and of the Transformers Qwen3 eager forward it mirrors.
 Each function cites the reference file:line it follows.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import it, and only as the checker (or the timed CPU baseline). The product
-path (kernel_optim_amd) never imports or calls anything here.
+import it, and only as the reference results are compared with (or the timed
+CPU baseline). The product path (kernel_optim_amd) never imports or calls
+anything here.
 
 Pinning (how each function is checked independently of its own formula):
 - attention.decode_attention: fp64 closed form; checked against torch SDPA
