@@ -432,6 +432,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
 #pragma unroll
       for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
     }
+    __builtin_amdgcn_sched_barrier(0);  // x and the gain stay ahead of the weights
 #pragma unroll
     for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
     __builtin_amdgcn_sched_barrier(0);
@@ -573,6 +574,7 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
 #pragma unroll
       for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
     }
+    __builtin_amdgcn_sched_barrier(0);  // x and the gain stay ahead of the weights
 #pragma unroll
     for (int s = 0; s < PD; ++s) issue(s, s);
     // keep the whole ring issued here: the scheduler would otherwise sink the
