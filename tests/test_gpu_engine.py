@@ -131,3 +131,18 @@ def test_engine_full_size_prompt1024_256_tokens(dev, B):
     print(f"full size B={B}: greedy agreement {agree:.4f} (prefill-shaped replay {agree_p:.4f}), "
           f"max |dlogit| {err:.4f}; reference decode- vs prefill-shaped {ref_noise:.4f}")
     assert err <= max(LOGIT_ATOL, 1.5 * ref_noise)
+
+
+def test_engine_from_a_transformers_checkpoint_directory(dev, tmp_path):
+    """Engine(model_path) on a directory written by Transformers' save_pretrained
+    (config.json + model.safetensors) decodes exactly as the engine built from the
+    same weights in memory."""
+    from kernel_optim_amd.engine import Engine
+    from tests.test_oracle_qwen3 import hf_model
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=34)
+    hf_model(cfg, w, "eager").save_pretrained(str(tmp_path), safe_serialization=True)
+    prompt = torch.randint(0, cfg.vocab, (2, 30), generator=torch.Generator().manual_seed(35)).tolist()
+    a = list(Engine(str(tmp_path)).generate(prompt, 8))
+    b = list(Engine.from_weights(cfg, w).generate(prompt, 8))
+    assert a == b and len(a) == 8
