@@ -141,8 +141,11 @@ def bench_decode(args, eng=None, B=1):
                      "achieved_gbs": round(step_bytes * tok_s / B / 1e9, 1),
                      "graph_step_frac": round((step_bytes / (step_ms * 1e-3) / 1e9) / PEAK_HBM_GBS, 4)},
         "first_tokens": out[:8],
-        "gemv_cfg": {k: [list(g.cfg), round(g.us, 2)] for k, g in eng.gv.items()},
+        "decode_graph": eng.step_kind,
+        "graph_ms_at_setup": eng.step_times,
     }
+    if eng.step_kind == "fused":
+        res["gemv_cfg"] = {k: [list(g.cfg), round(g.us, 2)] for k, g in eng.gv.items()}
     if not args.no_cpu and B == 1:
         res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
     return res

@@ -56,6 +56,11 @@ FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
 OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
+# decode-step graph: "auto" captures the fused-GEMV step and the hipBLASLt step for
+# batches up to FUSED_MAX_B and keeps the faster (engine.py:197-208); "fused" or
+# "hipblaslt" takes one
+DECODE_GRAPH = os.environ.get("ENGINE_DECODE_GRAPH", "auto")
+FUSED_MAX_B = 64     # fused-GEMV decode up to this batch; hipBLASLt beyond (engine.py:44)
 # speculative decoding by prompt lookup (engine.py:35-57)
 SPEC = os.environ.get("ENGINE_SPEC", "0") == "1"
 NGRAMS = (3, 2, 1)       # lookup order: the longest suffix first
@@ -146,7 +151,8 @@ def _log(msg):
 
 
 class Engine:
-    def __init__(self, model_path: str, keep_logits: bool = False, spec=None) -> None:
+    def __init__(self, model_path: str, keep_logits: bool = False, spec=None,
+                 decode_graph=None) -> None:
         self._t0 = time.monotonic()
         if model_path.startswith("random"):
             seed = int(model_path.split(":", 1)[1]) if ":" in model_path else 0
@@ -158,22 +164,29 @@ class Engine:
         else:
             cfg = Qwen3Config.from_hf_json(os.path.join(model_path, "config.json"))
             w = random_weights(cfg, seed=int(os.environ.get("ENGINE_SEED", "0")), device=DEVICE)
-        self._init(cfg, w, keep_logits, spec)
+        self._init(cfg, w, keep_logits, spec, decode_graph)
 
     @classmethod
-    def from_weights(cls, cfg, weights, keep_logits=False, spec=None):
+    def from_weights(cls, cfg, weights, keep_logits=False, spec=None, decode_graph=None):
         """Engine over weights already in the decode layout (moved to the GPU)."""
         from .model import weights_to
         self = cls.__new__(cls)
         self._t0 = time.monotonic()
-        self._init(cfg, weights_to(weights, DEVICE), keep_logits, spec)
+        self._init(cfg, weights_to(weights, DEVICE), keep_logits, spec, decode_graph)
         return self
 
-    def _init(self, cfg, w, keep_logits, spec=None):
+    def _init(self, cfg, w, keep_logits, spec=None, decode_graph=None):
         """spec: prompt-lookup speculation on (True) or off (False); None takes
-        ENGINE_SPEC (off unless set to 1)."""
+        ENGINE_SPEC (off unless set to 1). decode_graph: "auto" (time the fused
+        and the hipBLASLt decode graphs at setup and keep the faster; hipBLASLt
+        alone above FUSED_MAX_B), "fused" or "hipblaslt"; None takes
+        ENGINE_DECODE_GRAPH (auto unless set)."""
         self.spec = SPEC if spec is None else bool(spec)
         self.min_advance = MIN_ADVANCE   # None: the measured break-even
+        kind = DECODE_GRAPH if decode_graph is None else decode_graph
+        if kind not in ("auto", "fused", "hipblaslt"):
+            raise ValueError(f"decode_graph must be auto, fused or hipblaslt, not {kind!r}")
+        self.decode_graph = kind
         if cfg.head_dim != 128 or cfg.nq != 4 * cfg.nkv:
             raise ValueError("the decode kernels serve head_dim 128 with 4 query heads per KV head")
         self.cfg, self.w = cfg, w
@@ -222,8 +235,40 @@ class Engine:
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
                                     unit=ATTN_UNIT or None, fused_combine=True)
         self.attn.oproj_delay_ns = OPROJ_DELAY_NS
-        H, L = cfg.hidden, self.w["layers"]
-        e = cfg.eps
+        L = self.w["layers"]
+        raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],
+                   down=[l["down"] for l in L], lm=[self.w["lm_head"]])
+        deadline = time.monotonic() + TUNE_BUDGET_S
+        kind = self.decode_graph
+        if kind == "auto" and B > FUSED_MAX_B:
+            kind = "hipblaslt"
+        self.step_times = {}
+        g_fused = g_mm = None
+        if kind in ("auto", "fused"):
+            g_fused = self._setup_fused(raw, deadline)
+        if kind in ("auto", "hipblaslt"):
+            g_mm = self._setup_mm()
+        if g_fused is not None and g_mm is not None:
+            # keep whichever decode graph is faster here, measured during setup
+            self.g1 = g_fused
+            t_f = min(self._time_graph(g_fused) for _ in range(2))
+            self.g1 = g_mm
+            t_m = min(self._time_graph(g_mm) for _ in range(2))
+            self.step_times = {"fused_ms": round(t_f, 4), "hipblaslt_ms": round(t_m, 4)}
+            _log(f"decode step B={B}: fused {t_f * 1e3:.0f}us hipBLASLt {t_m * 1e3:.0f}us")
+            kind = "fused" if t_f < t_m else "hipblaslt"
+        self.step_kind = kind if kind != "auto" else "fused"
+        self.g1 = g_fused if self.step_kind == "fused" else g_mm
+        self.gk = None
+        if self.K:
+            self._setup_verify(raw, deadline)
+        self._shape = key
+
+    def _setup_fused(self, raw, deadline):
+        """The fused-GEMV decode step: tuned GEMVs (with MFMA weight copies where
+        the tuner takes them) and its captured graph."""
+        cfg, B = self.cfg, self.B
+        H, e = cfg.hidden, cfg.eps
         self.gv = dict(
             qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
             o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
@@ -231,9 +276,6 @@ class Engine:
             down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e),
             lm=Gemv(B, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
         )
-        raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],
-                   down=[l["down"] for l in L], lm=[self.w["lm_head"]])
-        deadline = time.monotonic() + TUNE_BUDGET_S
         self.gw = {}
         for name, g in self.gv.items():
             tiled = None
@@ -243,11 +285,17 @@ class Engine:
                 g.tune(raw[name], deadline, tiled=tiled)
                 _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
             self.gw[name] = tiled if uses_tiled(g.cfg) else raw[name]
-        self.g1 = self._capture(self._step1)
-        self.gk = None
-        if self.K:
-            self._setup_verify(raw, deadline)
-        self._shape = key
+        return self._capture(self._step1)
+
+    def _setup_mm(self):
+        """The hipBLASLt decode step (the reference's cuBLAS step, engine.py:388-401):
+        its buffers and captured graph."""
+        cfg, B, dev, bf = self.cfg, self.B, DEVICE, torch.bfloat16
+        self.nrm = torch.zeros(B, cfg.hidden, dtype=bf, device=dev)
+        self.gu_mm = torch.zeros(B, 2 * cfg.inter, dtype=bf, device=dev)
+        self.logits_mm = (self.logits if self.logits is not None
+                          else torch.zeros(B, cfg.vocab, dtype=bf, device=dev))
+        return self._capture(self._step1_mm)
 
     def _setup_verify(self, raw, deadline):
         """Buffers, GEMVs and the captured graph of the verify step, and the
@@ -346,6 +394,33 @@ class Engine:
             g["down"](self.act, W["down"][i], h=h)
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
                 pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
+
+    def _step1_mm(self):
+        """One decode token per sequence with hipBLASLt GEMMs (torch.mm) between
+        the fused ops: RMSNorm, the projections, the attention with its q/k norm +
+        RoPE + KV append prologue, SwiGLU, the residual adds, the LM head and the
+        greedy ids (argmax_rows); then positions advance and the chosen tokens'
+        embedding rows become the next step's input, as in the fused step."""
+        cfg = self.cfg
+        eps = cfg.eps
+        h = self.h   # holds embed[ids]
+        rope_rows(self.pos, self._cos, self._sin, self.rope)
+        for i, lw in enumerate(self.w["layers"]):
+            add_rms_norm(h, None, lw["w_in"], self.nrm, eps)
+            torch.mm(self.nrm, lw["qkv"].t(), out=self.qkv)
+            self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
+                                 self.pos, self.k_cache[i], self.v_cache[i], self.attn_out, eps,
+                                 rope=self.rope)
+            h.add_(torch.mm(self.attn_out, lw["o"].t()))   # h <- bf16(h + bf16(x @ W^T))
+            add_rms_norm(h, None, lw["w_post"], self.nrm, eps)
+            torch.mm(self.nrm, lw["gu"].t(), out=self.gu_mm)
+            silu_mul(self.gu_mm, self.act)
+            h.add_(torch.mm(self.act, lw["down"].t()))
+        add_rms_norm(h, None, self.w["final_norm"], self.nrm, eps)
+        torch.mm(self.nrm, self.w["lm_head"].t(), out=self.logits_mm)
+        argmax_rows(self.logits_mm, self.ids)
+        self.pos.add_(1)
+        embed_ss(self.ids, self.w["embed"], h, None)
 
     def _stepk(self):
         """Verify step (engine.py:403-416): vin[b] = [last accepted token, K drafts]

@@ -143,6 +143,27 @@ def test_config3_ragged_padded_tail_unread(dev):
     torch.testing.assert_close(out.float(), ref, **TOL)
 
 
+@pytest.mark.parametrize("fused_combine", [False, True])
+def test_more_than_64_sequences(dev, fused_combine):
+    """B = 130: the pair lookup past one wavefront's 64 lengths (three chunks of
+    lengths, the last partly filled), ragged lengths in 1..640, NaN beyond each."""
+    fused = _fused()
+    B, cap = 130, 640
+    g = torch.Generator().manual_seed(31)
+    lens = torch.randint(1, cap + 1, (B,), generator=g, dtype=torch.int32)
+    lens[0], lens[64], lens[129] = 1, cap, 17
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(32, 33, 34))
+    for b in range(B):
+        k[b, :, int(lens[b]):] = float("nan")
+        v[b, :, int(lens[b]):] = float("nan")
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev, fused_combine=fused_combine)
+    att.with_lengths(q, k, v, lens.to(dev), out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.float(), _gpu_ref_fp32(q, k, v, lens.tolist()), **TOL)
+
+
 def test_deterministic_and_unit_invariant(dev):
     fused = _fused()
     B, cap = 4, 3000

@@ -146,3 +146,67 @@ def test_engine_from_a_transformers_checkpoint_directory(dev, tmp_path):
     a = list(Engine(str(tmp_path)).generate(prompt, 8))
     b = list(Engine.from_weights(cfg, w).generate(prompt, 8))
     assert a == b and len(a) == 8
+
+
+def test_hipblaslt_decode_graph_matches_the_oracle(dev):
+    """The hipBLASLt decode graph (torch.mm projections between the fused ops),
+    forced, on the small config at B=2: greedy ids and logits as the fused graph's
+    bar, and generate() yields the traced tokens."""
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=5)
+    prompt = torch.randint(0, cfg.vocab, (2, 40), generator=torch.Generator().manual_seed(6))
+    n = 12
+    eng = _engine(cfg, w, decode_graph="hipblaslt")
+    toks, logits = eng.trace(prompt.tolist(), n)
+    assert eng.step_kind == "hipblaslt"
+    replay = Qwen3Oracle(cfg, w, B=2, cap=64).teacher_forced(prompt, toks)
+    agree, err = check_against_replay(toks, logits, replay)
+    assert agree == 1.0 and err < LOGIT_ATOL
+    out = list(eng.generate(prompt.tolist(), n))
+    assert torch.equal(torch.tensor(out).T, toks)
+
+
+def test_hipblaslt_decode_graph_qwen3_4b_width(dev):
+    cfg = Qwen3Config(layers=2)
+    w = random_weights(cfg, seed=7)
+    prompt = torch.randint(0, cfg.vocab, (3, 50), generator=torch.Generator().manual_seed(8))
+    n = 10
+    eng = _engine(cfg, w, decode_graph="hipblaslt")
+    toks, logits = eng.trace(prompt.tolist(), n)
+    replay = Qwen3Oracle(cfg, w, B=3, cap=64).teacher_forced(prompt, toks)
+    agree, err = check_against_replay(toks, logits, replay)
+    print(f"hipBLASLt graph, 2-layer Qwen3-4B width: agreement {agree:.3f}, max |dlogit| {err:.4f}")
+    assert err < LOGIT_ATOL
+
+
+def test_auto_keeps_the_faster_decode_graph(dev):
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=11)
+    prompt = torch.randint(0, cfg.vocab, (2, 16), generator=torch.Generator().manual_seed(12))
+    eng = _engine(cfg, w, decode_graph="auto")
+    toks, logits = eng.trace(prompt.tolist(), 6)
+    t = eng.step_times
+    assert set(t) == {"fused_ms", "hipblaslt_ms"}
+    assert eng.step_kind == ("fused" if t["fused_ms"] < t["hipblaslt_ms"] else "hipblaslt")
+    replay = Qwen3Oracle(cfg, w, B=2, cap=32).teacher_forced(prompt, toks)
+    agree, err = check_against_replay(toks, logits, replay)
+    assert agree == 1.0 and err < LOGIT_ATOL
+
+
+def test_batch_above_the_fused_limit_takes_hipblaslt(dev):
+    """B = FUSED_MAX_B + 1 = 65 sequences: auto selection sets
+    up only the hipBLASLt graph (the reference's rule, engine.py:197-199), and
+    every sequence's tokens and logits meet the oracle replay's bar."""
+    from kernel_optim_amd.engine import FUSED_MAX_B
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=13)
+    B = FUSED_MAX_B + 1
+    prompt = torch.randint(0, cfg.vocab, (B, 24), generator=torch.Generator().manual_seed(14))
+    n = 5
+    eng = _engine(cfg, w, decode_graph="auto")
+    toks, logits = eng.trace(prompt.tolist(), n)
+    assert eng.step_kind == "hipblaslt" and eng.step_times == {}
+    replay = Qwen3Oracle(cfg, w, B=B, cap=32).teacher_forced(prompt, toks)
+    agree, err = check_against_replay(toks, logits, replay)
+    print(f"B={B} hipBLASLt graph: agreement {agree:.3f}, max |dlogit| {err:.4f}")
+    assert err < LOGIT_ATOL
