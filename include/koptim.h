@@ -217,32 +217,6 @@ long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
  * graph. */
 int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, void* stream);
 
-/* Two layout-0 GEMVs of 1-2 rows in one launch, the second reading the first's
- * output; replaces two consecutive Gemv calls of the reference's fused decode
- * step (engine.py:288-289: gate/up then down, and engine.py:289 then :281: a
- * layer's down and the next layer's qkv). Results equal the two ko_gemv calls
- * (layout 0, `rows1` and `rows2` columns per workgroup).
- *   kind 0 (down -> qkv): out1 = h [M, N1] <- bf16(h + bf16(x [M, K1] @ w1^T)),
- *          then out2 [M, N2] = bf16(rmsnorm(h) * nw2 @ w2^T), w2 [N2, N1];
- *          rows1, rows2 in {4, 8}, rows2 also 16; K1 <= 10240, N1 <= 4096.
- *   kind 1 (gate/up -> down): out1 = act [M, N1] = SwiGLU of rmsnorm(x) * nw1 @
- *          w1^T (w1 [2 N1, K1] = gate | up), then out2 = h [M, N2] <- bf16(h +
- *          bf16(act @ w2^T)), w2 [N2, N1]; out2 may be x; rows1, rows2 in {4, 8};
- *          K1 <= 4096, N1 <= 10240.
- * N1 % 4 == 0. The second GEMV's workgroups issue their weight loads, then wait
- * (bounded; *err = 1 if a wait gives up) on a device-coherent flag raised when
- * every first-GEMV workgroup has stored its output. sync: ko_gemv_chain_sync_ints()
- * int32, 128-byte aligned, zero before the first call, left zero by every call;
- * calls sharing it must not overlap. delay_ns holds the second GEMV's weight
- * loads back after its start. */
-int ko_gemv_chain(int kind, const void* x, const void* w1, const void* nw1, void* out1,
-                  const void* w2, const void* nw2, void* out2, int M, int N1, int K1, int N2,
-                  int rows1, int rows2, float eps, int* sync, int* err, int delay_ns,
-                  void* stream);
-
-/* int32 elements of ko_gemv_chain's sync buffer (a size, not a status). */
-int ko_gemv_chain_sync_ints(void);
-
 /* Re-lays a row-major bf16 weight w [rows, K] into the tiled layout of ko_gemv
  * layout 2: wt holds ceil(rows/16)*16*K elements; for row tile t and k step s
  * (32 columns) the 1 KiB block at element ((t * K/32 + s) * 64 + l) * 8 holds,

@@ -52,15 +52,10 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                                  _c_void_p, _int, _c_void_p, _c_void_p],
     "ko_decode_attn_qkv_oproj_sync_ints": [],
-    "ko_gemv_chain": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                      _c_void_p, _int, _int, _int, _int, _int, _int, _f, _c_void_p, _c_void_p,
-                      _int, _c_void_p],
-    "ko_gemv_chain_sync_ints": [],
 }
 
 # Entry points whose return value is a size, not a status.
-RESTYPES = {"ko_gemv_argmax_scratch": _ll, "ko_decode_attn_qkv_oproj_sync_ints": _ll,
-            "ko_gemv_chain_sync_ints": _ll}
+RESTYPES = {"ko_gemv_argmax_scratch": _ll, "ko_decode_attn_qkv_oproj_sync_ints": _ll}
 
 _ERRORS = {-22: "invalid argument", -34: "size out of range", -95: "unsupported shape"}
 

@@ -1051,183 +1051,9 @@ long long parts_for(int N, int layout, int rows, int waves) {
   return ((units + waves - 1) / waves) * waves;
 }
 
-// ---------------------------------------------------------------------------
-// two chained row GEMVs in one launch
-// ---------------------------------------------------------------------------
-// Workgroups [0, nprod) run the first GEMV (layout 0, 1-2 rows of x) and write
-// its bf16 output with device-coherent stores, then count their arrival; the
-// one that completes the count raises CHAIN_FLAGS done-flag copies. The other
-// workgroups run the second GEMV over that output: they issue all their weight
-// loads, wait for their flag copy, then read the first GEMV's output with
-// device-scope loads (and its RMSNorm, for a NORM second GEMV). The second
-// projection's weights thus stream while the first one runs instead of after
-// it. Workgroups are dispatched in index order on each XCD, so every first-GEMV
-// workgroup is dispatched before any waiting one and none of them waits on
-// anything: the wait always ends. It is also bounded (SPIN_MAX polls, then *err
-// is set and the workgroup goes on). The counters re-arm themselves for the next
-// launch once every waiting workgroup is done.
-// Arrivals are counted in two levels (CHAIN_GROUPS counters, 128 bytes apart,
-// then one top count), since atomics on one address serialise.
-// sync[]: [0] first-GEMV groups done, [1] flag groups re-armed, then
-// CHAIN_FLAGS flag copies 128 bytes apart, each followed by the count of its
-// group's finished second-GEMV workgroups, then the CHAIN_GROUPS arrival counters.
-constexpr int CHAIN_FLAG0 = 32, CHAIN_FLAG_STRIDE = 32, CHAIN_FLAGS = 32, CHAIN_GROUPS = 32;
-constexpr int CHAIN_CTR0 = CHAIN_FLAG0 + CHAIN_FLAG_STRIDE * CHAIN_FLAGS;
-constexpr int CHAIN_SYNC_INTS = CHAIN_CTR0 + CHAIN_FLAG_STRIDE * CHAIN_GROUPS;
-constexpr int CHAIN_SPIN_MAX = 1 << 21;
-
-template <int M, bool PNORM, int PEPI, int PR, int PCPT, bool CNORM, int CEPI, int CR, int CCPT>
-__global__ __launch_bounds__(NT) void gemv_chain_kernel(GemvArgs p, GemvArgs c, int nprod,
-                                                        int* __restrict__ sync, int delay_ticks,
-                                                        int* __restrict__ err) {
-  if ((int)blockIdx.x < nprod) {
-    gemv_row_body<M, PR, PNORM, PEPI, PCPT, false, true>(p, blockIdx.x, [] {});
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent output stores are performed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int pg = blockIdx.x % CHAIN_GROUPS;
-      const int in_pg = (nprod - pg + CHAIN_GROUPS - 1) / CHAIN_GROUPS;
-      int* ctr = sync + CHAIN_CTR0 + CHAIN_FLAG_STRIDE * pg;
-      if (__hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-          in_pg - 1) {
-        // the group is complete: re-arm its counter (nothing else counts on it in
-        // this launch), then count the group
-        __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int groups = nprod < CHAIN_GROUPS ? nprod : CHAIN_GROUPS;
-        if (__hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            groups - 1) {
-          for (int f = 0; f < CHAIN_FLAGS; ++f)
-            __hip_atomic_store(sync + CHAIN_FLAG0 + CHAIN_FLAG_STRIDE * f, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-    return;
-  }
-  const int wg = blockIdx.x - nprod;
-  const int ncons = gridDim.x - nprod;
-  // Let the first GEMV's loads go ahead of this workgroup's weight stream.
-  if (delay_ticks > 0) {
-    const unsigned long long t0 = wall_clock64();
-    while (wall_clock64() - t0 < (unsigned long long)delay_ticks) __builtin_amdgcn_s_sleep(4);
-  }
-  const int grp = wg % CHAIN_FLAGS;
-  int* flag = sync + CHAIN_FLAG0 + CHAIN_FLAG_STRIDE * grp;
-  auto wait_x = [&] {
-    if (threadIdx.x == 0) {
-      int it = 0;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-        __builtin_amdgcn_s_sleep(8);
-        if (++it >= CHAIN_SPIN_MAX) {
-          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-      }
-    }
-    __syncthreads();
-  };
-  gemv_row_body<M, CR, CNORM, CEPI, CCPT, true>(c, wg, wait_x);
-  // Re-arm: the last workgroup of a flag group clears that flag and counts the
-  // group; the last group clears the arrival count and the group count.
-  if (threadIdx.x == 0) {
-    const int in_grp = (ncons - grp + CHAIN_FLAGS - 1) / CHAIN_FLAGS;
-    if (__hip_atomic_fetch_add(flag + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-        in_grp - 1) {
-      __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(flag + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int groups = ncons < CHAIN_FLAGS ? ncons : CHAIN_FLAGS;
-      if (__hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-          groups - 1) {
-        __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-}
-
-// The two chains the decode layer has: down (+ residual) -> next layer's qkv
-// (RMSNorm), and gate/up (RMSNorm, SwiGLU) -> down (+ residual).
-enum { CHAIN_DOWN_QKV = 0, CHAIN_GU_DOWN = 1 };
-
-template <int M, int PR, int CR>
-int launch_chain(int kind, const GemvArgs& p, const GemvArgs& c, int* sync, int ticks, int* err,
-                 hipStream_t s) {
-  const int nprod = (p.N + PR - 1) / PR, ncons = (c.N + CR - 1) / CR;
-  const dim3 grid(nprod + ncons), block(NT);
-  if (kind == CHAIN_DOWN_QKV) {
-    if constexpr (CR <= 16)
-      hipLaunchKernelGGL((gemv_chain_kernel<M, false, EPI_RESID, PR, 5, true, EPI_BF16, CR, 2>),
-                         grid, block, 0, s, p, c, nprod, sync, ticks, err);
-  } else {
-    if constexpr (CR <= 8)
-      hipLaunchKernelGGL((gemv_chain_kernel<M, true, EPI_SWIGLU, PR, 2, false, EPI_RESID, CR, 5>),
-                         grid, block, 0, s, p, c, nprod, sync, ticks, err);
-  }
-  return KO_LAUNCH_STATUS();
-}
-
-template <int M>
-int launch_chain_m(int kind, int pr, int cr, const GemvArgs& p, const GemvArgs& c, int* sync,
-                   int ticks, int* err, hipStream_t s) {
-  if (pr == 4 && cr == 4) return launch_chain<M, 4, 4>(kind, p, c, sync, ticks, err, s);
-  if (pr == 4 && cr == 8) return launch_chain<M, 4, 8>(kind, p, c, sync, ticks, err, s);
-  if (pr == 8 && cr == 4) return launch_chain<M, 8, 4>(kind, p, c, sync, ticks, err, s);
-  if (pr == 8 && cr == 8) return launch_chain<M, 8, 8>(kind, p, c, sync, ticks, err, s);
-  if (pr == 4 && cr == 16) return launch_chain<M, 4, 16>(kind, p, c, sync, ticks, err, s);
-  if (pr == 8 && cr == 16) return launch_chain<M, 8, 16>(kind, p, c, sync, ticks, err, s);
-  return KO_ENOTSUP;
-}
-
 }  // namespace
 
 extern "C" {
-
-int ko_gemv_chain_sync_ints(void) { return CHAIN_SYNC_INTS; }
-
-int ko_gemv_chain(int kind, const void* x, const void* w1, const void* nw1, void* out1,
-                  const void* w2, const void* nw2, void* out2, int M, int N1, int K1, int N2,
-                  int rows1, int rows2, float eps, int* sync, int* err, int delay_ns,
-                  void* stream) {
-  if (kind != CHAIN_DOWN_QKV && kind != CHAIN_GU_DOWN) return KO_EINVAL;
-  if (!x || !w1 || !out1 || !w2 || !out2 || !sync || !err) return KO_EINVAL;
-  if (M < 1 || M > 2 || N1 < 4 || (N1 & 3) || K1 < 8 || (K1 & 7) || N2 < 1) return KO_EINVAL;
-  if (!al16(x) || !al16(w1) || !al16(out1) || !al16(w2) || !al16(out2)) return KO_EINVAL;
-  if ((reinterpret_cast<uintptr_t>(sync) & 127u) != 0) return KO_EINVAL;
-  const bool norm1 = kind == CHAIN_GU_DOWN, norm2 = kind == CHAIN_DOWN_QKV;
-  if ((norm1 && (!nw1 || !al16(nw1))) || (norm2 && (!nw2 || !al16(nw2)))) return KO_EINVAL;
-  // row chunks per thread the kernels hold: 5 for the down projection's input
-  // width, 2 for the hidden width
-  const int kc_down = (kind == CHAIN_DOWN_QKV ? K1 : N1) / 8;
-  const int kc_hid = (kind == CHAIN_DOWN_QKV ? N1 : K1) / 8;
-  if (kc_down > 5 * NT || kc_hid > 2 * NT) return KO_ENOTSUP;
-  if (kind == CHAIN_GU_DOWN && rows2 > 8) return KO_ENOTSUP;
-  GemvArgs p = {}, c = {};
-  p.x = static_cast<const uint16_t*>(x);
-  p.w = static_cast<const uint16_t*>(w1);
-  p.nw = static_cast<const uint16_t*>(nw1);
-  p.mrows = M;
-  p.N = N1;
-  p.K = K1;
-  p.eps = eps;
-  c.x = static_cast<const uint16_t*>(out1);
-  c.w = static_cast<const uint16_t*>(w2);
-  c.nw = static_cast<const uint16_t*>(nw2);
-  c.mrows = M;
-  c.N = N2;
-  c.K = N1;
-  c.eps = eps;
-  if (kind == CHAIN_DOWN_QKV) {
-    p.h = static_cast<uint16_t*>(out1);  // h += down(x), in place
-    c.y = out2;
-  } else {
-    p.y = out1;
-    c.h = static_cast<uint16_t*>(out2);
-  }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int ticks = delay_ns > 0 ? delay_ns / 10 : 0;  // s_memrealtime runs at 100 MHz
-  return M == 1 ? launch_chain_m<1>(kind, rows1, rows2, p, c, sync, ticks, err, s)
-                : launch_chain_m<2>(kind, rows1, rows2, p, c, sync, ticks, err, s);
-}
 
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
             float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,

@@ -79,24 +79,6 @@ __device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float
   return 0.f;
 }
 
-// The bf16 output bits of element (m, n) for BF16 / SWIGLU / RESID (RESID reads
-// h[m, n] and returns the new residual), the value epilogue() stores.
-template <int EPI>
-__device__ __forceinline__ uint16_t epilogue_bits(const GemvArgs& a, int m, int n, float tot,
-                                                  float tot2) {
-  if constexpr (EPI == EPI_BF16) {
-    return f32_to_bf16(tot);
-  } else if constexpr (EPI == EPI_SWIGLU) {
-    const float g = round_bf16(tot), u = round_bf16(tot2);
-    const float s = round_bf16(g / (1.0f + expf(-g)));
-    return f32_to_bf16(s * u);
-  } else {
-    static_assert(EPI == EPI_RESID, "bf16 outputs only");
-    const float hn = round_bf16(bf16_to_f32(a.h[(long long)m * a.N + n]) + round_bf16(tot));
-    return f32_to_bf16(hn);
-  }
-}
-
 // layout 0 for 1-2 rows of x: the same mapping with the load order arranged
 // for the memory system. x (and the NORM gain) are loaded first and kept in
 // registers (normalised once), then every weight chunk of the workgroup is
@@ -110,21 +92,13 @@ __device__ __forceinline__ uint16_t epilogue_bits(const GemvArgs& a, int m, int 
 //
 // With XCOH the weights are issued first and `wait_x()` runs before x is read:
 // the caller's wait for the producer of x then overlaps the weight stream.
-// COH_OUT (BF16 / SWIGLU / RESID, R a multiple of 4, N a multiple of 4): the
-// outputs are written with device-coherent 8-byte stores (4 columns each), for
-// consumers later in the same launch; ss_out is not supported with it.
-template <int M, int R, bool NORM, int EPI, int CPT, bool XCOH, bool COH_OUT = false,
-          class WaitX>
+template <int M, int R, bool NORM, int EPI, int CPT, bool XCOH, class WaitX>
 __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&& wait_x) {
   constexpr int NW = EPI == EPI_SWIGLU ? 2 * R : R;
-  static_assert(!COH_OUT || ((EPI == EPI_BF16 || EPI == EPI_SWIGLU || EPI == EPI_RESID) &&
-                             R % 4 == 0),
-                "coherent outputs: bf16 epilogues, groups of 4 columns");
   __shared__ float red[16][M * NW];
   __shared__ float s_sq[GEMV_NT / 64][M];
   __shared__ float s_h2[M * R];
   __shared__ float2 s_best[M * R];
-  __shared__ __align__(8) uint16_t s_o[COH_OUT ? M * R : 1];
 
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int n0 = wg * R;
@@ -226,31 +200,12 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
       if constexpr (EPI == EPI_SWIGLU) tot2 += red[i][m * NW + R + r];
     }
     const bool ok = m < mr && n < N;
-    if constexpr (COH_OUT) {
-      s_o[idx] = ok ? epilogue_bits<EPI>(a, m, n, tot, tot2) : (uint16_t)0;
-      continue;
-    } else {
-      float h2 = 0.f;
-      if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
-      if constexpr (EPI == EPI_RESID) s_h2[idx] = h2;
-      if constexpr (EPI == EPI_ARGMAX)
-        s_best[idx] = make_float2(ok ? round_bf16(tot) : -INFINITY,
-                                  __int_as_float(ok ? n : 0x7fffffff));
-    }
-  }
-  if constexpr (COH_OUT) {
-    __syncthreads();
-    uint16_t* dst = EPI == EPI_RESID ? a.h : static_cast<uint16_t*>(a.y);
-    for (int q = t; q < M * (R / 4); q += GEMV_NT) {
-      const int m = q / (R / 4), n = n0 + 4 * (q - m * (R / 4));
-      if (m < mr && n < N) {
-        const unsigned long long v =
-            *reinterpret_cast<const unsigned long long*>(&s_o[m * R + (n - n0)]);
-        __hip_atomic_store(reinterpret_cast<unsigned long long*>(dst + (long long)m * N + n), v,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    return;
+    float h2 = 0.f;
+    if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+    if constexpr (EPI == EPI_RESID) s_h2[idx] = h2;
+    if constexpr (EPI == EPI_ARGMAX)
+      s_best[idx] = make_float2(ok ? round_bf16(tot) : -INFINITY,
+                                __int_as_float(ok ? n : 0x7fffffff));
   }
   if constexpr (EPI == EPI_RESID) {
     if (a.ss_out) {

@@ -205,53 +205,6 @@ class Gemv:
         return self.cfg
 
 
-CHAIN_DOWN_QKV, CHAIN_GU_DOWN = 0, 1
-
-
-class GemvChain:
-    """Two row GEMVs (layout 0, 1-2 rows) in one launch, the second reading the
-    first's output (ko_gemv_chain): the second projection's workgroups issue
-    their weight loads first and wait on a device-coherent flag for the first
-    one's output, so its weights stream while the first GEMV runs.
-      CHAIN_DOWN_QKV: h <- bf16(h + bf16(x @ w1^T)) (RESID), then
-                      y = bf16(rmsnorm(h) @ w2^T) (NORM, BF16): a layer's down
-                      projection and the next layer's qkv.
-      CHAIN_GU_DOWN:  act = swiglu(rmsnorm(x) @ w1^T) (NORM, SWIGLU), then
-                      h <- bf16(h + bf16(act @ w2^T)) (RESID): gate/up and down.
-    Results are those of the two ko_gemv calls (the same kernels' arithmetic).
-    The sync words re-arm themselves; calls on one object must not overlap."""
-
-    def __init__(self, kind, M, N1, K1, N2, device, rows=(4, 4), delay_ns=0, eps=1e-6):
-        _need(kind in (CHAIN_DOWN_QKV, CHAIN_GU_DOWN), "unknown chain")
-        _need(1 <= M <= 2, "a chain serves 1-2 rows")
-        self.kind, self.M, self.N1, self.K1, self.N2 = kind, M, N1, K1, N2
-        self.rows, self.delay_ns, self.eps = tuple(rows), delay_ns, eps
-        n = _lib.lib().ko_gemv_chain_sync_ints()
-        self.sync = torch.zeros(n, dtype=torch.int32, device=device)
-        self.err = torch.zeros(1, dtype=torch.int32, device=device)
-
-    def __call__(self, x, w1, nw1, out1, w2, nw2, out2):
-        """DOWN_QKV: x = act [M, K1], w1 = down [N1, K1], out1 = h [M, N1] (in place),
-        w2 = qkv [N2, N1], nw2 = its RMSNorm gain, out2 = y [M, N2].
-        GU_DOWN: x = h [M, K1], w1 = gate|up [2 N1, K1], nw1 = its gain, out1 = act
-        [M, N1], w2 = down [N2, N1], out2 = h [M, N2] (in place; may be x)."""
-        M, N1, K1, N2 = self.M, self.N1, self.K1, self.N2
-        down_qkv = self.kind == CHAIN_DOWN_QKV
-        _check(x, "x", BF16, (M, K1))
-        _check(w1, "w1", BF16, (N1 if down_qkv else 2 * N1, K1))
-        _check(out1, "out1", BF16, (M, N1))
-        _check(w2, "w2", BF16, (N2, N1))
-        _check(out2, "out2", BF16, (M, N2))
-        if down_qkv:
-            _check(nw2, "nw2", BF16, (N1,))
-        else:
-            _check(nw1, "nw1", BF16, (K1,))
-        _lib.call("ko_gemv_chain", self.kind, _lib.ptr(x), _lib.ptr(w1), _lib.ptr(nw1),
-                  _lib.ptr(out1), _lib.ptr(w2), _lib.ptr(nw2), _lib.ptr(out2), M, N1, K1, N2,
-                  self.rows[0], self.rows[1], self.eps, _lib.ptr(self.sync), _lib.ptr(self.err),
-                  self.delay_ns, _lib.stream_ptr())
-
-
 def tile_weights(w, swiglu=False):
     """The layout-2 (MFMA) copy of a row-major bf16 weight: [N, K] -> [ceil(N/16)*16, K]
     in the tiled order of ko_gemv_tile (one 1 KiB block per 16-row tile and 32-column
