@@ -83,7 +83,9 @@ class DecodeAttention:
         wg_split = T == 1
         if unit is None:
             share = _cdiv(_cdiv(B * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
-            unit = 4 * max(16, min(1024, share)) if wg_split else max(64, min(1024, share))
+            # one-token units stop at 2048 keys: past that, ragged lengths leave
+            # the last round of units unevenly filled
+            unit = 4 * max(16, min(512, share)) if wg_split else max(64, min(1024, share))
         _need(unit % 16 == 0 and unit >= 16, "unit must be a positive multiple of 16")
         self.unit = unit
         self.max_units = _cdiv(cap, unit)
