@@ -858,11 +858,13 @@ int launch_row(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
 
 template <int M, int R>
 int launch_block(const GemvArgs& a, int epi, bool norm, hipStream_t s) {
-  // 1-2 rows with K <= 10240: the register-resident row kernel
-  if constexpr (M <= 2 && R <= 8) {
+  // 1-4 rows with K <= 10240: the register-resident row kernel
+  if constexpr (M <= 4 && R <= 8) {
     const int KC = a.K >> 3;
     if (KC <= 2 * NT) return launch_row<M, R, 2>(a, epi, norm, s);
-    if (KC <= 5 * NT && !(epi == EPI_SWIGLU && R > 4)) return launch_row<M, R, 5>(a, epi, norm, s);
+    if constexpr (M <= 2 || R <= 4)
+      if (KC <= 5 * NT && !(epi == EPI_SWIGLU && R > 4))
+        return launch_row<M, R, 5>(a, epi, norm, s);
   }
   const dim3 grid((a.N + R - 1) / R), block(NT);
 #define KO_G(NORMV, EPIV) \

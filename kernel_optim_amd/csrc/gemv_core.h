@@ -79,7 +79,7 @@ __device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float
   return 0.f;
 }
 
-// layout 0 for 1-2 rows of x: the same mapping with the load order arranged
+// layout 0 for 1-4 rows of x: the same mapping with the load order arranged
 // for the memory system. x (and the NORM gain) are loaded first and kept in
 // registers (normalised once), then every weight chunk of the workgroup is
 // issued; loads return in issue order, so a dot product never waits behind a

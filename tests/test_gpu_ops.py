@@ -127,7 +127,7 @@ def _weights(dev, N, K, seed, rows=None):
 CFGS = [(0, 4, 0), (0, 8, 0), (1, 1, 2), (1, 2, 4), (1, 4, 2), (2, 1, 0), (2, 2, 0)]
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16])
 @pytest.mark.parametrize("cfg", CFGS)
 def test_gemv_epilogues(dev, M, cfg):
     _, gemv = K()
@@ -266,7 +266,8 @@ def test_gemv_split_k_layout(dev, M):
     assert {("o", 4), ("o", 8), ("down", 4), ("down", 19), ("qkv", 1), ("gu", 1)} <= seen
 
 
-@pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (16, (0, 8, 0)),
+@pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (3, (0, 8, 0)),
+                                   (4, (0, 4, 0)), (16, (0, 8, 0)),
                                    (3, (2, 1, 0)), (16, (2, 2, 0))])
 def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     _, gemv = K()
