@@ -86,6 +86,11 @@ class DecodeAttention:
             # one-token units stop at 2048 keys: past that, ragged lengths leave
             # the last round of units unevenly filled
             unit = 4 * max(16, min(512, share)) if wg_split else max(64, min(1024, share))
+            # ... unless one unit of 2048-4096 keys per CU covers the whole cache:
+            # then a single round of equal units, with the fewest partials to merge
+            per_cu = _cdiv(_cdiv(B * nkv * cap, max(1, target_ctas // 8)), 64) * 64
+            if wg_split and 2048 <= per_cu <= 4096:
+                unit = per_cu
         _need(unit % 16 == 0 and unit >= 16, "unit must be a positive multiple of 16")
         self.unit = unit
         self.max_units = _cdiv(cap, unit)
