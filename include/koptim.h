@@ -64,6 +64,19 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
                    float scale, float* o_part, float* ml, int* counters, void* out,
                    void* stream);
 
+/* DecodeAttention.__call__ for T = 2..8 query tokens per sequence (the verify
+ * step, engine/engine.py:407-410 with fused.py:221-234), computed as B*T rows of
+ * the one-token kernel: row b*T + t attends keys 0 .. pos[b] + t of sequence b
+ * (causal within the block, as ko_decode_attn with T tokens), and the last work
+ * unit of each (row, KV head) merges that row's partials (counters [B*T*nkv]
+ * int32, zero before the first call, left zero). o_part / ml are sized for
+ * B*T rows. Same results as ko_decode_attn to fp32 rounding; one launch. */
+int ko_decode_attn_token_rows(const void* q, const void* k_cache, const void* v_cache,
+                              const int* pos, int cap, long long cache_b_stride,
+                              long long cache_h_stride, int B, int T, int nkv, int head_dim,
+                              int unit, int max_units, int grid_waves, float scale,
+                              float* o_part, float* ml, int* counters, void* out, void* stream);
+
 /* One decode step of attention straight from the bf16 QKV projection
  * qkv [B, (nq+2nkv)*head_dim] (T = 1): per-head q/k RMSNorm (gains q_w, k_w,
  * eps) and RoPE (cos/sin [max_pos, head_dim] bf16) at position pos[b], append

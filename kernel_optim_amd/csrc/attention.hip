@@ -632,6 +632,26 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
   return launch_t<true>(a, T, grid_waves, static_cast<hipStream_t>(stream));
 }
 
+int ko_decode_attn_token_rows(const void* q, const void* k_cache, const void* v_cache,
+                              const int* pos, int cap, long long cache_b_stride,
+                              long long cache_h_stride, int B, int T, int nkv, int head_dim,
+                              int unit, int max_units, int grid_waves, float scale,
+                              float* o_part, float* ml, int* counters, void* out, void* stream) {
+  int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, T, nkv,
+                        head_dim, unit, max_units, o_part, ml);
+  if (st) return st;
+  if (T < 2 || !counters || !q || !aligned16(q) || !out || !aligned16(out) || grid_waves < 1)
+    return KO_EINVAL;
+  // row b * T + t: the one-token kernel over keys 0 .. pos[b] + t of sequence b
+  AttnArgs a = base_args(k_cache, v_cache, pos, 1, cap, cache_b_stride, cache_h_stride, B * T,
+                         nkv, unit, max_units, scale, o_part, ml);
+  a.rep = T;
+  a.q = static_cast<const uint16_t*>(q);
+  a.counters = counters;
+  a.out = static_cast<uint16_t*>(out);
+  return launch1<false, true>(a, grid_waves, static_cast<hipStream_t>(stream));
+}
+
 int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const void* cos,
                        const void* sin, int max_pos, const int* pos, void* k_cache,
                        void* v_cache, int cap, long long cache_b_stride,

@@ -48,6 +48,11 @@ struct AttnArgs {
   // tokens run in launches of up to 4 (attn_kernel's tile holds 4 tokens x 4
   // heads).
   int tstride, t0;
+  // Rows per sequence of the one-token kernel (1 normally): with rep > 1 row r
+  // is query token r % rep of sequence r / rep, reads that sequence's cache and
+  // sees lens[r / rep] + len_off + r % rep keys (the verify step's tokens run
+  // as rows of their own; no QKV prologue, fused merge only).
+  int rep;
   float scale_log2;
   float* o_part;
   float* ml;
@@ -61,18 +66,24 @@ struct AttnArgs {
 __device__ __forceinline__ int nunits(int len, int unit) {
   return len > 0 ? (len + unit - 1) / unit : 0;
 }
-__device__ __forceinline__ int seq_len(const int* lens, int b, int off, int cap) {
-  int l = lens[b] + off;
+__device__ __forceinline__ int seq_len(const int* lens, int b, int off, int cap, int rep = 1) {
+  int l;
+  if (rep == 1) {
+    l = lens[b] + off;
+  } else {
+    const int bc = b / rep;
+    l = lens[bc] + off + (b - bc * rep);
+  }
   return l < cap ? l : cap;
 }
 
 // Number of (b, c) pairs over the whole batch.
-__device__ inline int count_pairs(const int* lens, int off, int cap, int B, int unit) {
+__device__ inline int count_pairs(const int* lens, int off, int cap, int B, int unit, int rep = 1) {
   const int lane = lane_id();
   int tot = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int b = b0 + lane;
-    const int n = b < B ? nunits(seq_len(lens, b, off, cap), unit) : 0;
+    const int n = b < B ? nunits(seq_len(lens, b, off, cap, rep), unit) : 0;
     tot += readlane(wave_incl_scan(n), 63);
   }
   return tot;
@@ -80,12 +91,12 @@ __device__ inline int count_pairs(const int* lens, int off, int cap, int B, int 
 
 // Flattened pair index p -> (b, c).
 __device__ inline void locate_pair(int p, const int* lens, int off, int cap, int B, int unit,
-                            int& b_out, int& c_out) {
+                            int& b_out, int& c_out, int rep = 1) {
   const int lane = lane_id();
   int carry = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int b = b0 + lane;
-    const int n = b < B ? nunits(seq_len(lens, b, off, cap), unit) : 0;
+    const int n = b < B ? nunits(seq_len(lens, b, off, cap, rep), unit) : 0;
     const int incl = wave_incl_scan(n) + carry;
     const int tot = readlane(incl, 63);
     if (p < tot) {
@@ -304,11 +315,11 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     my_incl = readlane(my_n, 0);
     total = my_incl * nkv;
   } else if (small_b) {
-    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap), unit) : 0;
+    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap, a.rep), unit) : 0;
     my_incl = wave_incl_scan(my_n);
     total = readlane(my_incl, 63) * nkv;
   } else {
-    total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit) * nkv;
+    total = count_pairs(a.lens, a.len_off, a.cap, a.B, unit, a.rep) * nkv;
   }
   if constexpr (Hooks::kNotify)
     if (total == 0 && wg == 0) hooks.no_units();
@@ -325,13 +336,13 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     } else if (small_b) {
       b = uniform(__popcll(__ballot(my_incl <= pidx)));
       c = pidx - readlane(my_incl - my_n, b);
-      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap, a.rep));
     } else {
-      locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
+      locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c, a.rep);
       b = uniform(b);
       c = uniform(c);
       if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
-      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap, a.rep));
     }
     const int ku1 = min((c + 1) * unit, kv_len);
     const int k0 = c * unit + wave * sub;
@@ -350,8 +361,9 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
     }
 
-    const uint16_t* kb = a.kc + (long long)b * a.cb + (long long)kvh * a.ch;
-    const uint16_t* vb = a.vc + (long long)b * a.cb + (long long)kvh * a.ch;
+    const long long cb_off = (long long)(a.rep == 1 ? b : b / a.rep) * a.cb;  // its cache
+    const uint16_t* kb = a.kc + cb_off + (long long)kvh * a.ch;
+    const uint16_t* vb = a.vc + cb_off + (long long)kvh * a.ch;
     auto load_k = [&](int kk, uint4* kr) {
       const int key = min(kk + r, k1 - 1);
       const uint16_t* p = kb + (long long)key * D + 8 * g;
@@ -688,6 +700,7 @@ inline AttnArgs base_args(const void* k_cache, const void* v_cache, const int* l
   a.max_pos = 1;
   a.tstride = 1;
   a.t0 = 0;
+  a.rep = 1;
   return a;
 }
 

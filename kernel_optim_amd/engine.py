@@ -61,6 +61,9 @@ ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 # "hipblaslt" takes one
 DECODE_GRAPH = os.environ.get("ENGINE_DECODE_GRAPH", "auto")
 FUSED_MAX_B = 64     # fused-GEMV decode up to this batch; hipBLASLt beyond (engine.py:44)
+# verify-step attention: the K+1 tokens of a sequence as rows of the one-token
+# kernel (one launch) rather than T-token tiles (two launches and a merge)
+VERIFY_TOKEN_ROWS = os.environ.get("ENGINE_VERIFY_TOKEN_ROWS", "1") == "1"
 # speculative decoding by prompt lookup (engine.py:35-57)
 SPEC = os.environ.get("ENGINE_SPEC", "0") == "1"
 NGRAMS = (3, 2, 1)       # lookup order: the longest suffix first
@@ -315,9 +318,15 @@ class Engine:
         self.qT = torch.zeros(M, cfg.nq * cfg.head_dim, dtype=bf, device=dev)
         self.attT = torch.zeros_like(self.qT)
         self.actT = torch.zeros(M, cfg.inter, dtype=bf, device=dev)
-        # the merge as its own launch: one wavefront per row, where the fused
-        # combine would merge a pair's T x 4 rows in one wavefront
-        self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
+        if VERIFY_TOKEN_ROWS:
+            # the B*T tokens as rows of the one-token kernel, each row merged by
+            # its last unit: one launch
+            self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
+                                         fused_combine=True, token_rows=True)
+        else:
+            # T-token tiles and the merge as its own launch: one wavefront per row,
+            # where the fused combine would merge a pair's T x 4 rows in one wavefront
+            self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
         self.verify_fused = M <= FUSED_VERIFY_ROWS
         if self.verify_fused:   # one weight pass per projection on the fused GEMVs
             self.gvk = dict(

@@ -75,20 +75,26 @@ class DecodeAttention:
     MAX_T = 8
 
     def __init__(self, B, T, cap, nq, nkv, d, device, target_ctas=2048, unit=None,
-                 fused_combine=False):
+                 fused_combine=False, token_rows=False):
         _need(d == 128, "head_dim must be 128")
         _need(nq == 4 * nkv, "the kernel serves GQA groups of 4 query heads per KV head")
         _need(1 <= T <= self.MAX_T, f"T must be in 1..{self.MAX_T}")
+        _need(not token_rows or (T >= 2 and fused_combine),
+              "token_rows serves T >= 2 with the fused combine")
         self.B, self.T, self.cap, self.nq, self.nkv, self.d = B, T, cap, nq, nkv, d
-        wg_split = T == 1
+        # token_rows: the T tokens of a sequence run as T rows of the one-token
+        # kernel (ko_decode_attn_token_rows), each with its own causal length
+        self.token_rows = bool(token_rows)
+        wg_split = T == 1 or self.token_rows
+        rows_k = B * T if self.token_rows else B  # rows the one-token kernel sizes for
         if unit is None:
-            share = _cdiv(_cdiv(B * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
+            share = _cdiv(_cdiv(rows_k * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
             # one-token units stop at 2048 keys: past that, ragged lengths leave
             # the last round of units unevenly filled
             unit = 4 * max(16, min(512, share)) if wg_split else max(64, min(1024, share))
             # ... unless one unit of 2048-4096 keys per CU covers the whole cache:
             # then a single round of equal units, with the fewest partials to merge
-            per_cu = _cdiv(_cdiv(B * nkv * cap, max(1, target_ctas // 8)), 64) * 64
+            per_cu = _cdiv(_cdiv(rows_k * nkv * cap, max(1, target_ctas // 8)), 64) * 64
             if wg_split and 2048 <= per_cu <= 4096:
                 unit = per_cu
         _need(unit % 16 == 0 and unit >= 16, "unit must be a positive multiple of 16")
@@ -100,13 +106,14 @@ class DecodeAttention:
         else:
             wpu = 4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1
         self.waves_per_unit = wpu
-        self.grid_waves = max(1, min(B * nkv * self.max_units * wpu, target_ctas))
+        self.grid_waves = max(1, min(rows_k * nkv * self.max_units * wpu, target_ctas))
         rows = B * T * nq
         self.o_part = torch.empty(rows * self.max_units * d, dtype=torch.float32, device=device)
         self.ml = torch.empty(rows * self.max_units * 2, dtype=torch.float32, device=device)
-        # per-(sequence, KV head) arrival counters; every launch leaves them at zero
-        self.counters = (torch.zeros(B * nkv, dtype=torch.int32, device=device) if fused_combine
-                         else None)
+        # per-(sequence or token row, KV head) arrival counters; every launch leaves
+        # them at zero
+        self.counters = (torch.zeros(rows_k * nkv, dtype=torch.int32, device=device)
+                         if fused_combine else None)
         # decode_qkv_oproj: its counters and done flags, and its wait-failure flag
         self.sync = torch.zeros(_lib.lib().ko_decode_attn_qkv_oproj_sync_ints(), dtype=torch.int32,
                                 device=device)
@@ -135,17 +142,30 @@ class DecodeAttention:
     def __call__(self, q, k_cache, v_cache, pos, out):
         """q: [B*T, NQ*D]; k/v_cache: [B, NKV, cap, D]; pos: [B] int32 (first query
         position; keys 0..pos+T-1 are valid); out: [B*T, NQ*D]."""
+        if self.token_rows:
+            B, T, nq, nkv, d = self.B, self.T, self.nq, self.nkv, self.d
+            _check(q, "q", BF16, (B * T, nq * d))
+            _check(out, "out", BF16, (B * T, nq * d))
+            self._check_kv(k_cache, v_cache, pos)
+            _lib.call("ko_decode_attn_token_rows", _lib.ptr(q), _lib.ptr(k_cache),
+                      _lib.ptr(v_cache), _lib.ptr(pos), self.cap, k_cache.stride(0),
+                      k_cache.stride(1), B, T, nkv, d, self.unit, self.max_units,
+                      self.grid_waves, self.scale, _lib.ptr(self.o_part), _lib.ptr(self.ml),
+                      _lib.ptr(self.counters), _lib.ptr(out), _lib.stream_ptr())
+            return
         self._run(q, k_cache, v_cache, pos, self.T, out)
 
     def with_lengths(self, q, k_cache, v_cache, lengths, out):
         """Ragged form: lengths[b] = number of valid keys of sequence b (int32);
         the T queries sit at positions lengths[b]-T .. lengths[b]-1."""
+        _need(not self.token_rows, "with_lengths runs the T-token kernel (token_rows=False)")
         self._run(q, k_cache, v_cache, lengths, 0, out)
 
     def oproj_fusable(self):
         """decode_qkv_oproj serves 1-2 sequences with the fused combine and 4
         wavefronts per unit (attention.hip, ko_decode_attn_qkv_oproj)."""
-        return (self.B <= 2 and self.counters is not None and self.waves_per_unit == 4
+        return (self.T == 1 and self.B <= 2 and self.counters is not None
+                and self.waves_per_unit == 4
                 and self.nq * self.d <= 4096)
 
     def _check_rope(self, rope):

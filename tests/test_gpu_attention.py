@@ -96,6 +96,28 @@ def test_multi_token_causal(dev, T, fused_combine):
         assert torch.all(att.counters == 0)
 
 
+@pytest.mark.parametrize("B,T", [(1, 2), (1, 5), (1, 7), (3, 3), (3, 8), (12, 6)])
+def test_token_rows_causal(dev, B, T):
+    """The T tokens of each sequence as B*T rows of the one-token kernel
+    (ko_decode_attn_token_rows): row b*T + t sees keys 0..pos[b]+t. Against the
+    oracle's causal T-token attention; B*T = 72 takes the past-64-rows lookup."""
+    fused = _fused()
+    cap = 300
+    q, k, v = _inputs(B, T, cap, dev, seeds=(40, 41, 42))
+    g = torch.Generator().manual_seed(43)
+    first = torch.randint(0, cap - T + 1, (B,), generator=g).tolist()
+    first[0] = 0
+    pos = torch.tensor(first, dtype=torch.int32, device=dev)
+    att = fused.DecodeAttention(B, T, cap, 32, 8, 128, dev, fused_combine=True, token_rows=True)
+    want = A.decode_attention(q.cpu(), k.cpu(), v.cpu(), [p + T for p in first], T=T)
+    for _ in range(2):  # the counters re-arm between launches
+        out = torch.zeros_like(q)
+        att(q, k, v, pos, out)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().double(), want, **TOL)
+    assert torch.all(att.counters == 0)
+
+
 def test_config2_b16_ctx8192(dev):
     """Config 2: B=16 x 8192, against fp32 torch on the GPU for every sequence and
     the fp64 CPU oracle for four of them."""
