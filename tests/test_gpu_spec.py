@@ -61,16 +61,19 @@ def test_verify_step_matches_teacher_forced_oracle(dev, which, B):
     assert torch.all(best - chosen <= 2 * err + 1e-6)
 
 
-@pytest.mark.parametrize("B,min_advance", [(1, 0.0), (2, 0.0), (3, 0.0), (2, 1e9)])
-def test_spec_generate_emits_oracle_greedy_tokens(dev, B, min_advance):
+@pytest.mark.parametrize("B,min_advance,graph", [(1, 0.0, "auto"), (2, 0.0, "auto"),
+                                                 (3, 0.0, "auto"), (2, 1e9, "auto"),
+                                                 (2, 1e9, "hipblaslt")])
+def test_spec_generate_emits_oracle_greedy_tokens(dev, B, min_advance, graph):
     """min_advance 0: every step is a verify step; 1e9: the first acceptance check
-    (after 8 verify steps) hands decoding to the one-token graph."""
+    (after 8 verify steps) hands decoding to the one-token graph (graph: which
+    decode graph that is)."""
     cfg = SMALL
     w = perturbed_weights(cfg, seed=13)
     g = torch.Generator().manual_seed(14)
     prompt = torch.randint(0, cfg.vocab, (B, 8), generator=g).repeat(1, 5)  # lookup finds matches
     S, n = prompt.shape[1], 40
-    eng = _engine(cfg, w)
+    eng = _engine(cfg, w, decode_graph=graph)
     eng.min_advance = min_advance
     out = torch.tensor(list(eng.generate(prompt.tolist(), n))).T
     assert tuple(out.shape) == (B, n)
