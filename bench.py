@@ -138,6 +138,9 @@ def bench_decode(args, eng=None, B=1):
         "bytes_per_step": int(step_bytes),
         "roofline": {"bound": "hbm", "tok_s_at_peak": round(roof_tok_s, 1),
                      "frac": round(tok_s / roof_tok_s, 4),
+                     # weights alone (the KV cache reads left out of the bytes)
+                     "weights_only_frac": round(
+                         tok_s / (B * PEAK_HBM_GBS * 1e9 / cfg.weight_bytes_per_step()), 4),
                      "achieved_gbs": round(step_bytes * tok_s / B / 1e9, 1),
                      "graph_step_frac": round((step_bytes / (step_ms * 1e-3) / 1e9) / PEAK_HBM_GBS, 4)},
         "first_tokens": out[:8],
