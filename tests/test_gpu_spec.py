@@ -33,8 +33,11 @@ def _case(which, seed):
     return cfg, random_weights(cfg, seed=seed)
 
 
-@pytest.mark.parametrize("which,B", [("small", 1), ("small", 3), ("4b", 1), ("4b", 4)])
+@pytest.mark.parametrize("which,B", [("small", 1), ("small", 3), ("small", 16), ("small", 32),
+                                     ("4b", 1), ("4b", 4)])
 def test_verify_step_matches_teacher_forced_oracle(dev, which, B):
+    """B = 16 and 32 draft 4 and 2 tokens: 80 and 96 verify rows, on hipBLASLt,
+    with the attention's token rows past one wavefront's 64 lengths."""
     cfg, w = _case(which, 11)
     S, n = 40, 12
     prompt = torch.randint(0, cfg.vocab, (B, S), generator=torch.Generator().manual_seed(12))
@@ -42,7 +45,7 @@ def test_verify_step_matches_teacher_forced_oracle(dev, which, B):
     toks, _ = eng.trace(prompt.tolist(), n)
     K = eng.K
     T = K + 1
-    assert K == 6 and eng.verify_fused == (B * T <= 16)
+    assert K == (6 if B <= 4 else 4 if B <= 16 else 2) and eng.verify_fused == (B * T <= 16)
     x = torch.cat([prompt, toks], 1)
     j = 2                      # verify rows x[p0 .. p0+K], p0 the position of x[p0]
     p0 = S - 1 + j
