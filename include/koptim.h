@@ -9,7 +9,7 @@
  *     negative code if an argument was rejected on the host before launching:
  *       KO_EINVAL (-22) invalid pointer/size/alignment,
  *       KO_ERANGE (-34) a buffer too small for the requested shape,
- *       KO_ENOTSUP (-95) a shape this build does not serve (e.g. head_dim != 128).
+ *       KO_ENOTSUP (-95) a shape the library does not serve (e.g. head_dim != 128).
  * bf16 tensors are passed as void* to their raw 16-bit storage.
  */
 #ifndef KOPTIM_H
