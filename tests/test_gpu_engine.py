@@ -210,3 +210,20 @@ def test_batch_above_the_fused_limit_takes_hipblaslt(dev):
     agree, err = check_against_replay(toks, logits, replay)
     print(f"B={B} hipBLASLt graph: agreement {agree:.3f}, max |dlogit| {err:.4f}")
     assert err < LOGIT_ATOL
+
+
+@pytest.mark.parametrize("n", [1, 2, 3])
+@pytest.mark.parametrize("spec", [False, True])
+def test_generate_short_outputs(dev, n, spec):
+    """generate() yields exactly max_new_tokens lists of B ids (engine.py:418-533),
+    also for 1-3 tokens, where the first comes from the prefill and speculation
+    has no room to draft; the ids are the traced greedy ones."""
+    from kernel_optim_amd.engine import Engine
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=21)
+    prompt = torch.randint(0, cfg.vocab, (3, 10), generator=torch.Generator().manual_seed(22))
+    eng = Engine.from_weights(cfg, w, keep_logits=True, spec=spec)
+    out = list(eng.generate(prompt.tolist(), n))
+    assert len(out) == n and all(isinstance(x, list) and len(x) == 3 for x in out)
+    toks, _ = eng.trace(prompt.tolist(), n)
+    assert torch.equal(torch.tensor(out).T, toks)
