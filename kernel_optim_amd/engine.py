@@ -251,17 +251,15 @@ class Engine:
             g_fused = self._setup_fused(raw, deadline)
         if kind in ("auto", "hipblaslt"):
             g_mm = self._setup_mm()
-        if g_fused is not None and g_mm is not None:
+        if kind == "auto":
             # keep whichever decode graph is faster here, measured during setup
-            self.g1 = g_fused
             t_f = min(self._time_graph(g_fused) for _ in range(2))
-            self.g1 = g_mm
             t_m = min(self._time_graph(g_mm) for _ in range(2))
             self.step_times = {"fused_ms": round(t_f, 4), "hipblaslt_ms": round(t_m, 4)}
             _log(f"decode step B={B}: fused {t_f * 1e3:.0f}us hipBLASLt {t_m * 1e3:.0f}us")
             kind = "fused" if t_f < t_m else "hipblaslt"
-        self.step_kind = kind if kind != "auto" else "fused"
-        self.g1 = g_fused if self.step_kind == "fused" else g_mm
+        self.step_kind = kind
+        self.g1 = g_fused if kind == "fused" else g_mm
         self.gk = None
         if self.K:
             self._setup_verify(raw, deadline)
