@@ -53,7 +53,7 @@ TUNE = os.environ.get("ENGINE_TUNE", "1") == "1"
 TUNE_BUDGET_S = 60.0
 # attention and the o projection in one launch for 1-2 sequences (ENGINE_FUSE_OPROJ=0: two)
 FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
-OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
+OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "500"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 # decode-step graph: "auto" captures the fused-GEMV step and the hipBLASLt step for
