@@ -65,7 +65,7 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
                    void* stream);
 
 /* DecodeAttention.__call__ for T = 2..8 query tokens per sequence (the verify
- * step, engine/engine.py:407-410 with fused.py:221-234), computed as B*T rows of
+ * step, engine/engine.py:409-411 with fused.py:221-234), computed as B*T rows of
  * the one-token kernel: row b*T + t attends keys 0 .. pos[b] + t of sequence b
  * (causal within the block, as ko_decode_attn with T tokens), and the last work
  * unit of each (row, KV head) merges that row's partials (counters [B*T*nkv]
