@@ -42,10 +42,10 @@ def parse_args():
                     help="skip the ragged B=64 attention measurement (profiling B16 x 8K alone)")
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--new-tokens", type=int, default=256)
-    ap.add_argument("--decode-b16", action="store_true",
-                    help="also measure B=16 decode (same workload at batch 16)")
-    ap.add_argument("--layer", action="store_true",
-                    help="also measure one fused decoder layer at B=1, 4, 16 with 2048 cached keys")
+    ap.add_argument("--no-decode-b16", action="store_true",
+                    help="skip the B=16 decode measurement (same workload at batch 16)")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="skip the one-layer measurement (B=1, 4, 16 with 2048 cached keys)")
     ap.add_argument("--spec", action="store_true",
                     help="also measure B=1 decode with prompt-lookup speculation (the same "
                          "random prompt, and a prompt of a repeated 64-token pattern)")
@@ -194,21 +194,31 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     """One fused Qwen3-4B decoder layer decode step (qkv GEMV with RMSNorm prologue,
     attention with q/k norm + RoPE + KV append at position 2048, combine, o GEMV +
     residual, gate/up GEMV with RMSNorm + SwiGLU, down GEMV + residual), random
-    N(0, 0.02) weights, 2048 cached keys. ``nsets`` independent layers (weights and
-    caches) are rotated so the Infinity Cache cannot serve a replay; the replays
-    are captured in one graph and timed with events."""
+    N(0, 0.02) weights, 2048 cached keys: the engine's own layer body
+    (kernel_optim_amd.engine.decode_layer) with its tuned GEMVs. ``nsets``
+    independent layers (weights and caches) are rotated so the Infinity Cache
+    cannot serve a replay; the replays are captured in one graph and timed with
+    events."""
     import torch
+    from kernel_optim_amd.engine import _rope_tables, build_decode_gemvs, decode_layer
     from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
-    from kernel_optim_amd.kernels.gemv import (EPI_BF16, EPI_RESID, EPI_SWIGLU, Gemv, tile_weights,
-                                               uses_tiled)
-    from kernel_optim_amd.engine import _rope_tables
+    from kernel_optim_amd.kernels.gemv import tile_weights
     from kernel_optim_amd.model import Qwen3Config, random_weights
     cfg = Qwen3Config(layers=nsets)
     dev = torch.device("cuda:0")
     w = random_weights(cfg, seed=1, device=dev)
     cap = ctx + 16
     cos, sin = _rope_tables(cap, cfg.head_dim, cfg.theta, dev)
-    res, tiles = {}, {}
+    L = w["layers"]
+    raw = {name: [l[name] for l in L] for name in ("qkv", "o", "gu", "down")}
+    tiles = {}
+
+    def tiled_fn(name, ws):
+        if name not in tiles:
+            tiles[name] = [tile_weights(w_, swiglu=name == "gu") for w_ in ws]
+        return tiles[name]
+
+    res = {}
     for B in Bs:
         g = torch.Generator(device=dev).manual_seed(B)
         kc = [torch.randn(B, cfg.nkv, cap, cfg.head_dim, device=dev, generator=g).to(torch.bfloat16)
@@ -222,41 +232,16 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         # the engine's decode step: fused combine, the step's RoPE rows once, and the
         # o projection in the attention's launch where it fits (B <= 2)
         att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
+        att.oproj_delay_ns = 500
         rope = torch.empty(B, 2, cfg.head_dim, device=dev, dtype=torch.bfloat16)
         fuse_o = att.oproj_fusable()
-        H = cfg.hidden
-        L = w["layers"]
-        e = cfg.eps
-        ops = dict(qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
-                   o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
-                   gu=Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
-                   down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e))
-        W = {}
-        for name in ("qkv", "o", "gu", "down"):
-            raw = [l[name] for l in L]
-            tiled = None
-            if any(uses_tiled(c) for c in ops[name].candidates()):
-                tiled = tiles.setdefault(name, [tile_weights(w_, swiglu=name == "gu") for w_ in raw])
-            ops[name].tune(raw, time.monotonic() + 20, tiled=tiled)
-            W[name] = tiled if uses_tiled(ops[name].cfg) else raw
-
-        def layer(i):
-            lw = L[i]
-            ops["qkv"](h, W["qkv"][i], y=qkv, nw=lw["w_in"])
-            if fuse_o:
-                att.decode_qkv_oproj(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i],
-                                     att_out, cfg.eps, lw["o"], h, rope=rope)
-            else:
-                att.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, kc[i], vc[i],
-                               att_out, cfg.eps, rope=rope)
-                ops["o"](att_out, W["o"][i], h=h)
-            ops["gu"](h, W["gu"][i], y=act, nw=lw["w_post"])
-            ops["down"](act, W["down"][i], h=h)
+        ops, W = build_decode_gemvs(cfg, B, raw, time.monotonic() + 20, tiled_fn)
 
         def layers():
             rope_rows(pos, cos, sin, rope)
             for i in range(nsets):
-                layer(i)
+                decode_layer(ops, W, i, L[i], att, h, qkv, att_out, act, kc[i], vc[i], cos, sin,
+                             pos, rope, cfg.eps, fuse_o)
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -275,13 +260,15 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
             graph.replay()
         b.record()
         torch.cuda.synchronize()
+        att.check_sync()
         us = a.elapsed_time(b) * 1e3 / (reps * nsets)
         nbytes = cfg.layer_bytes() + B * (ctx + 1) * cfg.nkv * cfg.head_dim * 2 * 2 + \
             B * cfg.nkv * cfg.head_dim * 2 * 2
         res[f"B{B}"] = {"us_per_layer": round(us, 2), "bytes": int(nbytes),
                         "gbs": round(nbytes / us / 1e3, 1),
                         "roofline_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
-                        "gemv_cfgs": {k: v.cfg for k, v in ops.items()}}
+                        "gemv_cfgs": {k: v.cfg for k, v in ops.items() if k in W},
+                        "o_proj": "in the attention launch" if fuse_o else "own launch"}
         del kc, vc
         torch.cuda.empty_cache()
     return res
@@ -475,7 +462,7 @@ def main():
         from kernel_optim_amd.engine import Engine
         eng = Engine("random")
         line["decode_b1"] = bench_decode(args, eng, B=1)
-        if args.decode_b16:
+        if not args.no_decode_b16:
             line["decode_b16"] = bench_decode(args, eng, B=16)
         del eng
         torch.cuda.empty_cache()
@@ -487,7 +474,7 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_attn and not args.no_ragged:
         line["attention_ragged_b64"] = bench_attention_ragged()
-    if args.layer:
+    if not args.no_layer:
         line["layer_2048"] = bench_layer()
     print(json.dumps(line), flush=True)
 

@@ -8,6 +8,7 @@ import os
 import shutil
 import subprocess
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
@@ -20,7 +21,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # Packed fp32 VALU ops are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
@@ -38,24 +38,37 @@ def hipcc():
     raise RuntimeError("hipcc not found; the HIP extension cannot be built")
 
 
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-8000:]}")
+
+
 def build(verbose=False):
-    """Compile csrc/*.hip into kernel_optim_amd/libkoptim.so (atomic replace)."""
+    """Compile csrc/*.hip into kernel_optim_amd/libkoptim.so (atomic replace): each
+    source to an object in parallel, then one shared-library link."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    cc = hipcc()
     fd, tmp = tempfile.mkstemp(prefix=".libkoptim.", suffix=".so.tmp", dir=PKG_DIR)
     os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{CSRC}", *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+    objdir = tempfile.mkdtemp(prefix=".koobj.", dir=PKG_DIR)
     try:
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-8000:]}")
+        objs = [os.path.join(objdir, os.path.basename(src) + ".o") for src in srcs]
+        jobs = [[cc, *HIPCC_FLAGS, f"-I{CSRC}", "-c", src, "-o", obj]
+                for src, obj in zip(srcs, objs)]
+        with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1, 8)) as ex:
+            for f in [ex.submit(_run, cmd, verbose) for cmd in jobs]:
+                f.result()
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
         os.replace(tmp, LIB_PATH)
     finally:
         if os.path.exists(tmp):
             os.unlink(tmp)
+        shutil.rmtree(objdir, ignore_errors=True)
     return LIB_PATH
 
 

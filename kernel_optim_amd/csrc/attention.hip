@@ -474,6 +474,7 @@ __global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g,
   }
   const int grp = wg % OPROJ_FLAGS;
   int* flag = a.pairs_done + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * grp;
+  bool timed_out = false;  // thread 0 only
   auto wait_x = [&] {
     if (threadIdx.x == 0) {
       int it = 0;
@@ -481,6 +482,7 @@ __global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g,
         __builtin_amdgcn_s_sleep(8);
         if (++it >= SPIN_MAX) {
           __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          timed_out = true;
           break;
         }
       }
@@ -490,8 +492,11 @@ __global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g,
   gemv_row_body<M, 8, false, EPI_RESID, 2, true>(g, wg, wait_x);
   // Re-arm for the next launch, off the critical path: the last workgroup of a
   // flag group clears that flag and counts the group; the last group clears the
-  // pair count and the group count.
-  if (threadIdx.x == 0) {
+  // pair count and the group count. A workgroup whose wait gave up does not
+  // count itself: its group then never re-arms, so a merge that arrives late
+  // cannot be taken for the next launch's, and *err stays set until the host
+  // clears the sync words with it.
+  if (threadIdx.x == 0 && !timed_out) {
     const int in_grp = (nog - grp + OPROJ_FLAGS - 1) / OPROJ_FLAGS;  // workgroups of group grp
     if (__hip_atomic_fetch_add(flag + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
         in_grp - 1) {

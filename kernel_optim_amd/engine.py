@@ -6,9 +6,10 @@ yields one ``list[int]`` of length B per generated step, exactly
 ``max_new_tokens`` times, greedy, with no EOS stop.
 
 ``model_path`` is a local Hugging Face Qwen3 directory (config.json and
-*.safetensors), a directory with only config.json (random init), or
-``"random"`` / ``"random:<seed>"`` for the Qwen3-4B architecture with seeded
-N(0, 0.02) weights.
+*.safetensors), or ``"random"`` / ``"random:<seed>"`` for the Qwen3-4B
+architecture with seeded N(0, 0.02) weights. A directory with only config.json
+raises FileNotFoundError unless ENGINE_RANDOM_INIT=1 asks for random weights
+over that config (seed ENGINE_SEED).
 
 Per shape (B, S, N) the engine allocates a static KV cache
 [layers, B, 8, cap, 128] bf16, prefills the prompt with PyTorch-ROCm ops
@@ -153,6 +154,59 @@ def _log(msg):
         print(f"[engine] {msg}", file=sys.stderr, flush=True)
 
 
+def build_decode_gemvs(cfg, M, raw, deadline, tiled_fn=None, tune=True, log=""):
+    """The decode step's five fused projections for M rows (the reference's
+    _setup_fused set, engine.py:256-262, with the LM head's greedy selection
+    fused in): qkv (RMSNorm prologue, bf16 out), o (+ residual), gate/up (RMSNorm
+    prologue, SwiGLU), down (+ residual), LM head (RMSNorm prologue, ARGMAX).
+    ``raw`` maps each name to its per-layer row-major weights; with ``tune`` each
+    Gemv is timed over them (Gemv.tune). ``tiled_fn(name, weights)`` returns the
+    MFMA-tiled copies for a projection that has tiled candidates (None: tune
+    makes them). Returns (gemvs, weights in each one's launch layout)."""
+    H, e = cfg.hidden, cfg.eps
+    gv = dict(
+        qkv=Gemv(M, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
+        o=Gemv(M, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
+        gu=Gemv(M, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
+        down=Gemv(M, H, cfg.inter, EPI_RESID, norm=False, eps=e),
+        lm=Gemv(M, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
+    )
+    W = {}
+    for name, g in gv.items():
+        if name not in raw:
+            continue
+        tiled = None
+        if any(uses_tiled(c) for c in g.candidates()):
+            tiled = (tiled_fn(name, raw[name]) if tiled_fn is not None
+                     else [tile_weights(w, swiglu=name == "gu") for w in raw[name]])
+        if tune:
+            g.tune(raw[name], deadline, tiled=tiled)
+            _log(f"{log}gemv {name} M={M} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
+        W[name] = tiled if uses_tiled(g.cfg) else raw[name]
+    return gv, W
+
+
+def decode_layer(gv, W, i, lw, attn, h, qkv, attn_out, act, k_cache, v_cache, cos, sin, pos,
+                 rope, eps, fuse_o):
+    """Layer i of the one-token decode step (engine.py:278-287 in this package's
+    launches): qkv GEMV (RMSNorm prologue) -> attention (q/k norm + RoPE + KV
+    append at pos, split-K partials, last-unit merge), with the o projection and
+    its residual add in the same launch when ``fuse_o`` -> o GEMV (+ residual)
+    otherwise -> gate/up GEMV (RMSNorm prologue, SwiGLU) -> down GEMV (+ residual).
+    h [B, H] is the residual stream, updated in place; k_cache/v_cache are the
+    layer's [B, nkv, cap, d] slices; rope the step's RoPE rows (rope_rows)."""
+    gv["qkv"](h, W["qkv"][i], y=qkv, nw=lw["w_in"])
+    if fuse_o:
+        attn.decode_qkv_oproj(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, k_cache, v_cache,
+                              attn_out, eps, lw["o"], h, rope=rope)
+    else:
+        attn.decode_qkv(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, k_cache, v_cache,
+                        attn_out, eps, rope=rope)
+        gv["o"](attn_out, W["o"][i], h=h)
+    gv["gu"](h, W["gu"][i], y=act, nw=lw["w_post"])
+    gv["down"](act, W["down"][i], h=h)
+
+
 class Engine:
     def __init__(self, model_path: str, keep_logits: bool = False, spec=None,
                  decode_graph=None) -> None:
@@ -164,9 +218,17 @@ class Engine:
         elif os.path.isdir(model_path) and any(f.endswith(".safetensors")
                                                 for f in os.listdir(model_path)):
             cfg, w = load_checkpoint(model_path, device=DEVICE)
-        else:
+        elif os.environ.get("ENGINE_RANDOM_INIT", "0") == "1":
+            # a config-only directory, random weights asked for explicitly
             cfg = Qwen3Config.from_hf_json(os.path.join(model_path, "config.json"))
-            w = random_weights(cfg, seed=int(os.environ.get("ENGINE_SEED", "0")), device=DEVICE)
+            seed = int(os.environ.get("ENGINE_SEED", "0"))
+            print(f"[engine] {model_path}: random N(0, 0.02) weights, seed {seed} "
+                  "(ENGINE_RANDOM_INIT=1)", file=sys.stderr, flush=True)
+            w = random_weights(cfg, seed=seed, device=DEVICE)
+        else:
+            raise FileNotFoundError(
+                f"{model_path}: no *.safetensors weights (pass 'random[:seed]' or set "
+                "ENGINE_RANDOM_INIT=1 for random weights over its config.json)")
         self._init(cfg, w, keep_logits, spec, decode_graph)
 
     @classmethod
@@ -268,24 +330,8 @@ class Engine:
     def _setup_fused(self, raw, deadline):
         """The fused-GEMV decode step: tuned GEMVs (with MFMA weight copies where
         the tuner takes them) and its captured graph."""
-        cfg, B = self.cfg, self.B
-        H, e = cfg.hidden, cfg.eps
-        self.gv = dict(
-            qkv=Gemv(B, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
-            o=Gemv(B, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
-            gu=Gemv(B, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
-            down=Gemv(B, H, cfg.inter, EPI_RESID, norm=False, eps=e),
-            lm=Gemv(B, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
-        )
-        self.gw = {}
-        for name, g in self.gv.items():
-            tiled = None
-            if any(uses_tiled(c) for c in g.candidates()):
-                tiled = self._tiled(name, raw[name])
-            if TUNE:
-                g.tune(raw[name], deadline, tiled=tiled)
-                _log(f"gemv {name} B={B} cfg={g.cfg} {g.us:.1f}us candidates={g.tune_log}")
-            self.gw[name] = tiled if uses_tiled(g.cfg) else raw[name]
+        self.gv, self.gw = build_decode_gemvs(self.cfg, self.B, raw, deadline, self._tiled,
+                                              tune=TUNE)
         return self._capture(self._step1)
 
     def _setup_mm(self):
@@ -327,22 +373,8 @@ class Engine:
             self.attnk = DecodeAttention(B, T, self.cap, cfg.nq, cfg.nkv, cfg.head_dim, dev)
         self.verify_fused = M <= FUSED_VERIFY_ROWS
         if self.verify_fused:   # one weight pass per projection on the fused GEMVs
-            self.gvk = dict(
-                qkv=Gemv(M, cfg.nqkv, H, EPI_BF16, norm=True, eps=e),
-                o=Gemv(M, H, cfg.nq * cfg.head_dim, EPI_RESID, norm=False, eps=e),
-                gu=Gemv(M, cfg.inter, H, EPI_SWIGLU, norm=True, eps=e),
-                down=Gemv(M, H, cfg.inter, EPI_RESID, norm=False, eps=e),
-                lm=Gemv(M, cfg.vocab, H, EPI_ARGMAX, norm=True, eps=e),
-            )
-            self.gwk = {}
-            for name, g in self.gvk.items():
-                tiled = None
-                if any(uses_tiled(c) for c in g.candidates()):
-                    tiled = self._tiled(name, raw[name])
-                if TUNE:
-                    g.tune(raw[name], deadline, tiled=tiled)
-                    _log(f"verify gemv {name} M={M} cfg={g.cfg} {g.us:.1f}us")
-                self.gwk[name] = tiled if uses_tiled(g.cfg) else raw[name]
+            self.gvk, self.gwk = build_decode_gemvs(cfg, M, raw, deadline, self._tiled,
+                                                    tune=TUNE, log="verify ")
         else:                   # hipBLASLt GEMMs between the fused ops
             self.nT = torch.zeros(M, H, dtype=bf, device=dev)
             self.guT = torch.zeros(M, 2 * cfg.inter, dtype=bf, device=dev)
@@ -387,18 +419,9 @@ class Engine:
         fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
         rope_rows(self.pos, self._cos, self._sin, self.rope)  # the step's RoPE rows, once
         for i, lw in enumerate(self.w["layers"]):
-            g["qkv"](h, W["qkv"][i], y=self.qkv, nw=lw["w_in"])
-            if fuse_o:  # attention + o projection + residual in one launch
-                self.attn.decode_qkv_oproj(self.qkv, lw["q_norm"], lw["k_norm"], self._cos,
-                                           self._sin, self.pos, self.k_cache[i], self.v_cache[i],
-                                           self.attn_out, cfg.eps, lw["o"], h, rope=self.rope)
-            else:
-                self.attn.decode_qkv(self.qkv, lw["q_norm"], lw["k_norm"], self._cos, self._sin,
-                                     self.pos, self.k_cache[i], self.v_cache[i], self.attn_out,
-                                     cfg.eps, rope=self.rope)
-                g["o"](self.attn_out, W["o"][i], h=h)
-            g["gu"](h, W["gu"][i], y=self.act, nw=lw["w_post"])
-            g["down"](self.act, W["down"][i], h=h)
+            decode_layer(g, W, i, lw, self.attn, h, self.qkv, self.attn_out, self.act,
+                         self.k_cache[i], self.v_cache[i], self._cos, self._sin, self.pos,
+                         self.rope, cfg.eps, fuse_o)
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
                 pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
 
@@ -561,6 +584,8 @@ class Engine:
                 ids_h[j + 1].copy_(self.ids, non_blocking=True)
                 ev[j + 1].record(stream)
             ev[j].synchronize()
+            if j == N - 1:
+                self.attn.check_sync()   # raises if a fused o-projection wait gave up
             yield ids_h[j].tolist()
 
     def _generate_spec(self, input_ids, N, stream):
@@ -629,10 +654,12 @@ class Engine:
             ev[j].record(stream)
             if j > 1:
                 emitted = yield from self._drain(j - 1, outs, N, emitted)
-        emitted = yield from self._drain(todo, outs, N, emitted)
+        emitted = yield from self._drain(todo, outs, N, emitted, last=True)
 
-    def _drain(self, j, outs, N, emitted):
+    def _drain(self, j, outs, N, emitted, last=False):
         self.events[j].synchronize()
+        if last:
+            self.attn.check_sync()
         for b, t in enumerate(self.pin_ids[j].tolist()):
             outs[b].append(t)
         ready = min(N, min(len(o) for o in outs))
@@ -656,4 +683,5 @@ class Engine:
             self.g1.replay()
             toks.append(self.ids.cpu())
             logits.append(self.logits.cpu())
+        self.attn.check_sync()
         return torch.stack(toks, 1), logits

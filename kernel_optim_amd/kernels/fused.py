@@ -161,6 +161,23 @@ class DecodeAttention:
         _need(not self.token_rows, "with_lengths runs the T-token kernel (token_rows=False)")
         self._run(q, k_cache, v_cache, lengths, 0, out)
 
+    def check_sync(self):
+        """Raise RuntimeError if a decode_qkv_oproj launch since the last check gave
+        up its wait for the attention (its results are then invalid). Reads one
+        int32 from the device, so it synchronises; before raising it clears the
+        sync words, the arrival counters and the flag, so the next launch starts
+        clean."""
+        if int(self.err.item()) == 0:
+            return
+        torch.cuda.synchronize(self.err.device)
+        self.sync.zero_()
+        self.err.zero_()
+        if self.counters is not None:
+            self.counters.zero_()
+        torch.cuda.synchronize(self.err.device)
+        raise RuntimeError("decode attention + o projection: the projection's wait for the "
+                           "attention timed out; the results of those calls are invalid")
+
     def oproj_fusable(self):
         """decode_qkv_oproj serves 1-2 sequences with the fused combine and 4
         wavefronts per unit (attention.hip, ko_decode_attn_qkv_oproj)."""

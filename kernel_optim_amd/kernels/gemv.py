@@ -19,12 +19,22 @@ Additions of this backend:
 ``cfg`` is an opaque tuple ``(layout, rows, waves)``: layout 0 gives each
 256-thread workgroup ``rows`` output columns (any M); layout 1 gives each
 wavefront ``rows`` columns with ``waves`` wavefronts per workgroup sharing the
-normalised input through LDS (M <= 4). ``allow_split`` is accepted for
-signature compatibility; the kernels never split K (each work unit streams
-full rows), so the F32 epilogue is a plain store.
+normalised input through LDS (M <= 4); layouts 2 and 3 put 2..16 rows on MFMA
+tiles and read a tiled copy of the weights (``tile_weights``), layout 3 with
+the K range of a tile cut into ``rows`` slices merged by the tile's last slice
+(no atomics on the output, so the F32 epilogue is a plain store).
+``allow_split`` is accepted for signature compatibility.
+
+Drop-in rule for the tiled layouts: the default configuration (``cfg`` before
+``tune``) is always a row-major layout, ``tune(weights, deadline)`` makes the
+tiled copies itself when it times a tiled candidate (and keeps them, keyed by
+the row-major weight), and ``__call__`` maps a row-major weight to its copy
+when the configuration needs one. A tiled configuration on a weight with no
+copy, or a tiled copy under a row-major configuration, raises ValueError.
 """
 
 import time
+import weakref
 
 import torch
 
@@ -39,6 +49,11 @@ def uses_tiled(cfg):
     return cfg[0] in (2, 3)
 
 
+def is_tiled(w):
+    """True for a tensor written by tile_weights (the MFMA-layout copy)."""
+    return getattr(w, "_ko_tiled", False)
+
+
 class Gemv:
     """One fused projection y[M, N] = x[M, K] @ W[N, K]^T with a norm prologue and
     an epilogue; its launch config is picked by GPU timing at setup."""
@@ -50,7 +65,9 @@ class Gemv:
         self.allow_split = allow_split
         self.cfg = self.candidates()[0]
         self._part = None
+        self._tiles = {}   # id(row-major weight) -> (weakref to it, its tiled copy)
         self.us = float("nan")
+        self.tune_log = []
 
     def mfma_ok(self):
         """Layout 2 (MFMA tiles, x rows padded to 16) takes K in {2560, 4096, 9728},
@@ -70,16 +87,15 @@ class Gemv:
         return [s for s in out if s == 1 and self.K == 2560] if self.norm else out
 
     def candidates(self):
-        """Launch configurations, the default first. Layout 1 (a wavefront per row
-        group) is the batch-1..4 path; layout 0 serves every batch up to 16 rows
-        per launch with VALU dot products; layout 2 puts 2..16 rows on MFMA
-        (``(2, per_cu, 0)``: a persistent grid of 256 x per_cu workgroups)."""
+        """Launch configurations, the default first. The default is always a
+        row-major layout, so an untuned Gemv runs on the weights the caller holds.
+        Layout 1 (a wavefront per row group) is the batch-1..4 path; layout 0
+        serves every batch up to 16 rows per launch with VALU dot products;
+        layout 2 puts 2..16 rows on MFMA (``(2, per_cu, 0)``: a persistent grid
+        of 256 x per_cu workgroups) and layout 3 splits its tiles' K range."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
         mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
-        if self.M > 4:
-            out += mfma
-            mfma = []
         if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):
             per_wave = (4, 2, 1) if self.N >= 32768 else (1, 2, 4)
             for rows in per_wave:
@@ -99,6 +115,25 @@ class Gemv:
             self._part = torch.zeros(max(n, 2), dtype=torch.float32, device=device)
         return self._part
 
+    def _weight_for(self, w, cfg):
+        """The weight tensor this configuration reads: ``w`` itself, or for a tiled
+        layout the copy ``tune`` made of the row-major ``w``."""
+        if uses_tiled(cfg):
+            if is_tiled(w):
+                return w
+            ent = self._tiles.get(id(w))
+            if ent is not None and ent[0]() is w:
+                return ent[1]
+            raise ValueError(f"cfg {cfg} reads MFMA-tiled weights, but this weight has no tiled "
+                             "copy: pass tile_weights(w) or tune() with these weights")
+        _need(not is_tiled(w), f"cfg {cfg} reads row-major weights, got a tile_weights copy")
+        return w
+
+    def _remember_tiles(self, weights, tiled):
+        for w, t in zip(weights, tiled):
+            if not is_tiled(w):
+                self._tiles[id(w)] = (weakref.ref(w), t)
+
     def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None,
                  pos_inc=None, next_emb=None, next_h=None):
         """ARGMAX extras: ``pos_inc`` ([M] int32) is advanced by one; with
@@ -107,6 +142,7 @@ class Gemv:
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
+        w = self._weight_for(w, (layout, rows, waves))
         nrows = _cdiv(N, 16) * 16 if uses_tiled((layout,)) else N  # the tile_weights copy
         _check(w, "w", BF16, ((2 * nrows) if epi == EPI_SWIGLU else nrows, K))
         if self.norm:
@@ -146,9 +182,17 @@ class Gemv:
         graphs are captured first and timed in ``rounds`` interleaved rounds, each
         candidate keeping its best round, so drift and one-off noise do not decide
         the choice; a candidate replaces an earlier (default-first) one only when
-        it is more than 1 % faster. Layout-2 candidates run on ``tiled`` (the
-        tile_weights copies of ``weights``) and are skipped without it."""
+        it is more than 1 % faster. Tiled (MFMA) candidates run on ``tiled`` (the
+        tile_weights copies of ``weights``); without it, tune makes the copies
+        itself (before the deadline) and keeps them, so a later call with a
+        row-major weight of ``weights`` reads its copy. With the deadline passed
+        nothing is timed and the configuration stays the row-major default."""
         dev = weights[0].device
+        if any(uses_tiled(c) for c in self.candidates()):
+            if tiled is None and time.monotonic() <= deadline:
+                tiled = [tile_weights(w, swiglu=self.epi == EPI_SWIGLU) for w in weights]
+            if tiled is not None:
+                self._remember_tiles(weights, tiled)
         M, N, K = self.M, self.N, self.K
         x = torch.randn(M, K, device=dev, dtype=BF16)
         y = torch.zeros(M, N, device=dev, dtype=torch.float32 if self.epi == EPI_F32 else BF16)
@@ -183,6 +227,8 @@ class Gemv:
                 continue
             graphs.append((cfg, g))
         cfgs = [c for c, _ in graphs]
+        if not graphs:
+            return self.cfg
         times = [float("inf")] * len(graphs)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for _ in range(rounds):
@@ -222,6 +268,7 @@ def tile_weights(w, swiglu=False):
     for i, part in enumerate(halves):
         _lib.call("ko_gemv_tile", _lib.ptr(part), _lib.ptr(out[i * npad:(i + 1) * npad]), n, K,
                   _lib.stream_ptr())
+    out._ko_tiled = True
     return out
 
 

@@ -63,7 +63,9 @@ class Qwen3Oracle:
         self.cos, self.sin = (t.to(device) for t in rope_tables(cap, d, cfg.theta))
 
     @torch.no_grad()
-    def forward(self, ids, start):
+    def forward(self, ids, start, hidden=False):
+        """bf16 logits [B, T, V]; with ``hidden`` the residual stream after the last
+        layer instead (before the final norm), [B, T, H]."""
         cfg, w = self.cfg, self.w
         B, T = ids.shape
         nq, nkv, d, I = cfg.nq, cfg.nkv, cfg.head_dim, cfg.inter
@@ -93,6 +95,8 @@ class Qwen3Oracle:
             gu = lw["gu"]
             mlp = F.linear(F.silu(F.linear(hn, gu[:I])) * F.linear(hn, gu[I:]), lw["down"])
             x = res + mlp
+        if hidden:
+            return x
         x = rmsnorm(x, w["final_norm"], cfg.eps)
         return F.linear(x, w["lm_head"])
 

@@ -13,6 +13,14 @@ from tests.test_oracle_qwen3 import SMALL, hf_greedy, hf_model, perturbed_weight
 pytestmark = pytest.mark.gpu
 TIE_MARGIN = 2.0
 LOGIT_ATOL = 0.25
+# Full 36-layer depth, random N(0, 0.02) weights, hundreds of decode steps: the
+# reference eager path is itself 0.20-0.22 logits away from its own replay with
+# other GEMM shapes (decode-shaped against prefill-shaped), so the stated bar is
+# a flat 0.35 logits, and at least 85 % of the tokens must be the reference's
+# greedy choice (measured 0.90-0.94; the rest are near-ties within the 2x-error
+# rule).
+FULL_LOGIT_ATOL = 0.35
+FULL_AGREEMENT_MIN = 0.85
 
 
 def _engine(cfg, w, **kw):
@@ -100,21 +108,22 @@ def test_two_generate_calls_do_not_share_state(dev):
     assert a == a2 and len(b) == 6 and all(len(x) == 2 for x in b)
 
 
-@pytest.mark.parametrize("B", [1, 16])
-def test_engine_full_size_prompt1024_256_tokens(dev, B):
+@pytest.mark.parametrize("B,S", [(1, 1024), (16, 1024), (4, 2048)])
+def test_engine_full_size_decode(dev, B, S):
     """The decode workload at full size: Qwen3-4B architecture (36 layers, random
-    N(0, 0.02) bf16 weights), prompts of 1024 seeded random ids, 256 greedy tokens.
-    The reference eager path replays the emitted tokens decode-shaped (one forward
-    per token, as generate() with a KV cache runs): every token must be within the
-    tie margin and the 2x-error rule. The prefill-shaped replay (one forward over
-    the whole sequence) measures the reference path's own bf16 rounding noise under
-    a change of GEMM shapes (ref_noise = max |decode-shaped - prefill-shaped|); the
-    engine's logits must be within max(LOGIT_ATOL, 1.5 * ref_noise) of the
-    decode-shaped replay: no further from the reference than the reference is from
-    itself, with half again as margin."""
+    N(0, 0.02) bf16 weights), prompts of S seeded random ids, 256 greedy tokens;
+    B = 1 and 16 at S = 1024 (the benchmark's decode workloads) and B = 4 at
+    S = 2048 (the reference contract's public batch-4 workload,
+    QWEN_ENGINE_CONTRACT.md:79). The reference eager path replays the emitted
+    tokens decode-shaped (one forward per token, as generate() with a KV cache
+    runs): every token must be within the tie margin and the 2x-error rule, the
+    logits within FULL_LOGIT_ATOL and the greedy agreement at least
+    FULL_AGREEMENT_MIN. The prefill-shaped replay (one forward over the whole
+    sequence) is printed beside it: the reference path's own bf16 rounding noise
+    under a change of GEMM shapes."""
     cfg = Qwen3Config()
     w = random_weights(cfg, seed=0, device=dev)
-    S, n = 1024, 256
+    n = 256
     prompt = torch.randint(0, cfg.vocab, (B, S), generator=torch.Generator().manual_seed(B))
     eng = _engine(cfg, w)
     toks, logits = eng.trace(prompt.tolist(), n)
@@ -128,9 +137,11 @@ def test_engine_full_size_prompt1024_256_tokens(dev, B):
     ref_noise = float((replay.float() - prefill_shaped.float()).abs().max())
     agree, err = check_against_replay(toks, logits, replay)
     agree_p = float((prefill_shaped.float().argmax(-1) == toks).float().mean())
-    print(f"full size B={B}: greedy agreement {agree:.4f} (prefill-shaped replay {agree_p:.4f}), "
-          f"max |dlogit| {err:.4f}; reference decode- vs prefill-shaped {ref_noise:.4f}")
-    assert err <= max(LOGIT_ATOL, 1.5 * ref_noise)
+    print(f"full size B={B} S={S}: greedy agreement {agree:.4f} (prefill-shaped replay "
+          f"{agree_p:.4f}), max |dlogit| {err:.4f}; reference decode- vs prefill-shaped "
+          f"{ref_noise:.4f}")
+    assert err <= FULL_LOGIT_ATOL
+    assert agree >= FULL_AGREEMENT_MIN
 
 
 def test_engine_from_a_transformers_checkpoint_directory(dev, tmp_path):
