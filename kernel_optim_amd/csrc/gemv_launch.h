@@ -1,0 +1,54 @@
+// Launchers of the four GEMV layouts, compiled in their own sources
+// (gemv_block.hip: layout 0; gemv_wave.hip: layout 1; gemv_mfma.hip: layouts 2
+// and 3) and called
+// by the C entry points in gemv.hip, plus the shape rules those entry points
+// validate against.
+#pragma once
+
+#include "gemv_core.h"
+
+namespace ko {
+
+constexpr int LDS_X_BYTES = 40960;  // layout 1: normalised x staged for the workgroup (M*K*2)
+constexpr int MFMA_CUS = 256;       // MI355X compute units: layout-2 persistent grid = 256 x rows
+constexpr int KS_MAX = 32;          // layout 3: slices per tile
+
+// layout 0: `rows` (4, 8; 16 for M <= 2) columns per 256-thread workgroup
+int launch_layout0(const GemvArgs& a, int epi, bool norm, int rows, hipStream_t s);
+// layout 1: `rw` columns per wavefront, `wpb` wavefronts per workgroup
+int launch_layout1(const GemvArgs& a, int epi, bool norm, int rw, int wpb, hipStream_t s);
+// layout 2: MFMA tiles, a persistent grid of MFMA_CUS * per_cu workgroups
+int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s);
+// layout 3: MFMA tiles with the K range cut into `slices`
+int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                   hipStream_t s);
+
+inline int mfma_grid(int N, int per_cu) {
+  const int ntiles = (N + 15) / 16;
+  const int g = MFMA_CUS * per_cu;
+  return ntiles < g ? ntiles : g;
+}
+
+// K = 32 * S * WPG: S steps of 32 per wavefront, WPG wavefronts splitting K.
+// SWIGLU (two weight tiles) needs K <= 4096 to keep its registers.
+inline bool mfma_supported(int K, int epi) {
+  return K == 2560 || K == 4096 || (K == 9728 && epi != EPI_SWIGLU);
+}
+
+// Steps per wavefront of layout 3 for K and a slice count (0: unsupported):
+// S in {20, 19, 8, 4} with K = 128 * S * slices.
+inline int ks_steps(int K, int slices) {
+  if (slices < 1 || slices > KS_MAX || K % (128 * slices)) return 0;
+  const int S = K / (128 * slices);
+  return (S == 20 || S == 19 || S == 8 || S == 4) ? S : 0;
+}
+
+// Layout 3 scratch (fp32 elements): the tiles' arrival counters (int32, zero
+// before the first launch, left at zero by every launch), padded to 64, then
+// two 16 x 16 fp32 slots (gate and up) per (tile, slice).
+inline long long ks_scratch(int N, int slices) {
+  const long long T = (N + 15) / 16;
+  return ((T + 63) / 64) * 64 + T * slices * 2 * 256;
+}
+
+}  // namespace ko

@@ -1,0 +1,425 @@
+// Fused skinny GEMM, MFMA layouts 2 and 3 (v_mfma_f32_16x16x32_bf16 on the
+// tiled weight copy); the semantics are those of gemv.hip's entry points
+// (engine/kernels/gemv.py:30-106).
+#include "gemv_launch.h"
+
+using namespace ko;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// layout 2: MFMA tiles of 16 columns, x rows padded to 16
+// ---------------------------------------------------------------------------
+
+// Row-wise (16-lane) argmax of (value, index): lowest index on ties.
+__device__ __forceinline__ void row_argmax16(float& v, int& i) {
+#define KO_ARG_STEP(CTRL)                                                                  \
+  {                                                                                        \
+    const float ov = dpp_f<CTRL>(v);                                                       \
+    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xf, 0xf, false);               \
+    if (ov > v || (ov == v && oi < i)) {                                                   \
+      v = ov;                                                                              \
+      i = oi;                                                                              \
+    }                                                                                      \
+  }
+  KO_ARG_STEP(0x128)
+  KO_ARG_STEP(0x124)
+  KO_ARG_STEP(0x122)
+  KO_ARG_STEP(0x121)
+#undef KO_ARG_STEP
+}
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+template <int EPI, bool NORM, int S, int PD, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int ntiles) {
+  static_assert(S % PD == 0, "the weight ring must tile the K steps");
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
+  __shared__ float s_c[WPG][NW][16][17];
+  __shared__ float s_sq[WPG][16];
+
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, mr = a.mrows;
+  const int G = gridDim.x;
+  const int kw0 = wv * (32 * S) + 8 * g;  // this lane's first k (step s adds 32 s)
+  const bool mok = col < mr;               // A row m = col exists
+
+  // Ring of PD weight steps in flight. The weights are in the tiled layout
+  // (ko_gemv_tile): the B operand of (tile, step) is one 1 KiB block with lane
+  // l's 16 bytes at 16 l, and a wavefront's steps are consecutive blocks.
+  const int T = (N + 15) / 16, KS = K / 32;
+  const uint16_t* wlane = a.w + (long long)(wv * S) * 512 + 8 * lane;
+  uint4 wb[PD][NW];
+  auto issue = [&](int tile, int s, int slot) {
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + s) * 512);
+  };
+  // This wavefront's K slice of x (A operand, row m = col), kept in registers
+  // for every tile; NORM normalises it once. x (and, where registers allow, the
+  // NORM gain) is loaded first, then the first tile's weights: loads return in
+  // issue order, so the prologue runs while the weights stream. The weights
+  // stay issued there (the scheduler would otherwise sink the loads next to
+  // their MFMAs to save registers).
+  constexpr bool NW_EARLY = NORM && S <= 10;
+  bf16x8 xa[S];
+  {
+    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+    uint4 xr[S], nwv[NW_EARLY ? S : 1];
+#pragma unroll
+    for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NW_EARLY) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // x and the gain stay ahead of the weights
+#pragma unroll
+    for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+      float rstd;
+      if (a.ss) {
+        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+      } else {
+        float sq = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) sq += sq8(xr[s]);
+        sq = sum_xor32(sum_xor16(sq));  // the 4 lane groups of row m
+        if (g == 0) s_sq[wv][col] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) tot += s_sq[w][col];
+        rstd = rsqrtf(tot / (float)K + a.eps);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        uint4 w;
+        if constexpr (NW_EARLY) w = nwv[s];
+        else w = ldg16(a.nw + kw0 + 32 * s);
+        xr[s] = norm8(xr[s], w, rstd);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
+  }
+
+  float bv = -INFINITY;  // ARGMAX: running best of row t / 16 (threads with t % 16 == 0)
+  int bi = 0x7fffffff;
+  // The wavefronts' partial tiles summed through LDS, then the epilogue, one
+  // thread per (m, n).
+  auto finish = [&](int tile, const f32x4* c) {
+    // C lane layout: column col, rows 4g + i.
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_c[wv][r][4 * g + i][col] = c[r][i];
+    __syncthreads();
+    if (t < 256) {
+      const int m = t >> 4, j = t & 15, n = tile * 16 + j;
+      float tot = 0.f, tot2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) {
+        tot += s_c[w][0][m][j];
+        if constexpr (NW == 2) tot2 += s_c[w][NW - 1][m][j];
+      }
+      const bool ok = m < mr && n < N;
+      float h2 = 0.f;
+      if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+      if constexpr (EPI == EPI_RESID) {
+        if (a.ss_out) {
+          h2 = row_sum16(h2);
+          if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+        }
+      }
+      if constexpr (EPI == EPI_ARGMAX) {
+        float v = ok ? round_bf16(tot) : -INFINITY;
+        int vi = ok ? n : 0x7fffffff;
+        row_argmax16(v, vi);
+        if (v > bv || (v == bv && vi < bi)) {
+          bv = v;
+          bi = vi;
+        }
+      }
+    }
+    __syncthreads();  // s_c is rewritten by the next tile
+  };
+  // One tile. Each consumed slot is refilled with the step PD ahead: of this
+  // tile, or with ISSUE of the next one. The workgroup's last tile runs without
+  // ISSUE, so nothing is loaded past it. (Re-issuing a clamped tile there
+  // instead cost ~4.5 us of the 16-row gate/up GEMV's ~25.)
+  auto run = [&](auto issue_c, int tile, int next) {
+    constexpr bool ISSUE = decltype(issue_c)::value != 0;
+    f32x4 c[NW];
+#pragma unroll
+    for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int slot = s % PD;
+#pragma unroll
+      for (int r = 0; r < NW; ++r)
+        c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
+                                                       c[r], 0, 0, 0);
+      if (s + PD < S) issue(tile, s + PD, slot);
+      else if constexpr (ISSUE) issue(next, s + PD - S, slot);
+    }
+    finish(tile, c);
+  };
+
+  int tile = blockIdx.x;
+  for (; tile + G < ntiles; tile += G) run(IntC<1>{}, tile, tile + G);
+  if (tile < ntiles) run(IntC<0>{}, tile, tile);
+  if constexpr (EPI == EPI_ARGMAX) {
+    const int m = t >> 4;
+    if (t < 256 && (t & 15) == 0 && m < mr)
+      a.part[(long long)m * a.nparts + blockIdx.x] = make_float2(bv, __int_as_float(bi));
+  }
+}
+
+// layout 3: the layout-2 weight tiles with the K range of a tile cut into
+// slices, one 4-wavefront workgroup per (tile, slice), a grid of
+// ntiles * slices workgroups (not persistent). Wavefront w of slice q takes the
+// S consecutive 32-wide K steps starting at (4 q + w) S, so slices = K / (128 S).
+// With one slice the workgroup runs the epilogue itself. With more, each writes
+// its fp32 16 x 16 partial tile to its own slot with device-coherent stores and
+// counts its arrival on the tile's counter; the last to arrive adds the slots
+// in slice order (the result does not depend on the arrival order), re-arms
+// the counter and runs the epilogue. NORM computes the row norms from the
+// wavefronts' x slices, so it needs one slice (or ss given).
+constexpr int KSW = 4;       // wavefronts per workgroup of layout 3
+template <int EPI, bool NORM, int S, int PD>
+__global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int* __restrict__ ctr,
+                                                               float* __restrict__ slots) {
+  static_assert(EPI != EPI_ARGMAX, "the split-K layout has no argmax epilogue");
+  constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
+  __shared__ float s_c[KSW][NW][16][17];
+  __shared__ float s_sq[KSW][16];
+  __shared__ int s_prev;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, mr = a.mrows;
+  const int nsl = K / (32 * S * KSW);
+  const int tile = blockIdx.x / nsl, slice = blockIdx.x - tile * nsl;
+  const int T = (N + 15) / 16, KS = K / 32;
+  const int sb = (slice * KSW + wv) * S;  // this wavefront's first K step
+  const int kw0 = sb * 32 + 8 * g;        // this lane's first k
+  const bool mok = col < mr;
+
+  const uint16_t* wlane = a.w + 8 * lane;
+  uint4 wb[PD][NW];
+  auto issue = [&](int s, int slot) {
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + sb + s) * 512);
+  };
+
+  // x (and the NORM gain) first: loads return in issue order, so the prologue
+  // then runs while the weights stream instead of after them.
+  bf16x8 xa[S];
+  {
+    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+    uint4 xr[S], nwv[NORM ? S : 1];
+#pragma unroll
+    for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // x and the gain stay ahead of the weights
+#pragma unroll
+    for (int s = 0; s < PD; ++s) issue(s, s);
+    // keep the whole ring issued here: the scheduler would otherwise sink the
+    // weight loads next to their MFMAs to save registers, leaving ~3 in flight
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+      float rstd;
+      if (a.ss) {
+        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+      } else {  // one slice: the KSW wavefronts hold the whole row
+        float sq = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) sq += sq8(xr[s]);
+        sq = sum_xor32(sum_xor16(sq));
+        if (g == 0) s_sq[wv][col] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < KSW; ++w) tot += s_sq[w][col];
+        rstd = rsqrtf(tot / (float)K + a.eps);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], nwv[s], rstd);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
+  }
+
+  f32x4 c[NW];
+#pragma unroll
+  for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int slot = s % PD;
+#pragma unroll
+    for (int r = 0; r < NW; ++r)
+      c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
+                                                     c[r], 0, 0, 0);
+    if (s + PD < S) issue(s + PD, slot);
+  }
+  // C lane layout: column col, rows 4g + i.
+#pragma unroll
+  for (int r = 0; r < NW; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_c[wv][r][4 * g + i][col] = c[r][i];
+  __syncthreads();
+  const int m = t >> 4, j = t & 15, n = tile * 16 + j;
+  float tot = 0.f, tot2 = 0.f;
+#pragma unroll
+  for (int w = 0; w < KSW; ++w) {
+    tot += s_c[w][0][m][j];
+    if constexpr (NW == 2) tot2 += s_c[w][NW - 1][m][j];
+  }
+  if (nsl > 1) {
+    float* mine = slots + ((long long)(tile * nsl + slice) * NW) * 256 + t;
+    __hip_atomic_store(mine, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (NW == 2) __hip_atomic_store(mine + 256, tot2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's slot stores are performed
+    __syncthreads();
+    if (t == 0) s_prev = __hip_atomic_fetch_add(ctr + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_prev != nsl - 1) return;
+    const float* base = slots + (long long)tile * nsl * NW * 256 + t;
+    float v[KS_MAX], v2[KS_MAX];
+#pragma unroll
+    for (int q = 0; q < KS_MAX; ++q) {
+      v[q] = q < nsl ? __hip_atomic_load(base + q * NW * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      if constexpr (NW == 2)
+        v2[q] = q < nsl ? __hip_atomic_load(base + q * NW * 256 + 256, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+    tot = 0.f;
+    tot2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < KS_MAX; ++q) {
+      if (q < nsl) {
+        tot += v[q];
+        if constexpr (NW == 2) tot2 += v2[q];
+      }
+    }
+    if (t == 0) __hip_atomic_store(ctr + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool ok = m < mr && n < N;
+  float h2 = 0.f;
+  if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+  if constexpr (EPI == EPI_RESID) {
+    if (a.ss_out) {
+      h2 = row_sum16(h2);
+      if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+    }
+  }
+}
+
+template <int S, int PD, int WPG>
+int launch_mfma_s(const GemvArgs& a, int epi, bool norm, int grid, hipStream_t s) {
+  const int ntiles = (a.N + 15) / 16;
+#define KO_M(NORMV, EPIV)                                                             \
+  hipLaunchKernelGGL((gemv_mfma_kernel<EPIV, NORMV, S, PD, WPG>), dim3(grid), dim3(64 * WPG), 0, \
+                     s, a, ntiles)
+  if (norm) {
+    switch (epi) {
+      case EPI_F32: KO_M(true, EPI_F32); break;
+      case EPI_BF16: KO_M(true, EPI_BF16); break;
+      case EPI_RESID: KO_M(true, EPI_RESID); break;
+      case EPI_SWIGLU: KO_M(true, EPI_SWIGLU); break;
+      default: KO_M(true, EPI_ARGMAX); break;
+    }
+  } else {
+    switch (epi) {
+      case EPI_F32: KO_M(false, EPI_F32); break;
+      case EPI_BF16: KO_M(false, EPI_BF16); break;
+      case EPI_RESID: KO_M(false, EPI_RESID); break;
+      case EPI_SWIGLU: KO_M(false, EPI_SWIGLU); break;
+      default: KO_M(false, EPI_ARGMAX); break;
+    }
+  }
+#undef KO_M
+  return KO_LAUNCH_STATUS();
+}
+
+
+int launch_mfma(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s) {
+  const int grid = mfma_grid(a.N, per_cu);
+  switch (a.K) {
+    case 2560: return launch_mfma_s<10, 10, 8>(a, epi, norm, grid, s);
+    case 4096: return launch_mfma_s<16, 16, 8>(a, epi, norm, grid, s);
+    default:
+      if (epi == EPI_SWIGLU) return KO_ENOTSUP;
+      return launch_mfma_s<38, 19, 8>(a, epi, norm, grid, s);
+  }
+}
+
+
+template <int S, int PD>
+int launch_mfma_ks_s(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                     hipStream_t s) {
+  const int grid = ((a.N + 15) / 16) * slices;
+#define KO_K(NORMV, EPIV)                                                                  \
+  hipLaunchKernelGGL((gemv_mfma_ks_kernel<EPIV, NORMV, S, PD>), dim3(grid), dim3(64 * KSW), 0, s, \
+                     a, ctr, slots)
+  if (norm) {
+    if constexpr (S == 20) {
+      switch (epi) {
+        case EPI_F32: KO_K(true, EPI_F32); break;
+        case EPI_BF16: KO_K(true, EPI_BF16); break;
+        case EPI_RESID: KO_K(true, EPI_RESID); break;
+        default: KO_K(true, EPI_SWIGLU); break;
+      }
+    } else {
+      return KO_ENOTSUP;
+    }
+  } else {
+    switch (epi) {
+      case EPI_F32: KO_K(false, EPI_F32); break;
+      case EPI_BF16: KO_K(false, EPI_BF16); break;
+      case EPI_RESID: KO_K(false, EPI_RESID); break;
+      default: KO_K(false, EPI_SWIGLU); break;
+    }
+  }
+#undef KO_K
+  return KO_LAUNCH_STATUS();
+}
+
+int launch_mfma_ks(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                   hipStream_t s) {
+  // every weight step in flight at once, except SWIGLU's two tiles at 20 steps
+  // (registers)
+  switch (ks_steps(a.K, slices)) {
+    case 20:
+      if (epi == EPI_SWIGLU) return launch_mfma_ks_s<20, 10>(a, epi, norm, slices, ctr, slots, s);
+      return launch_mfma_ks_s<20, 20>(a, epi, norm, slices, ctr, slots, s);
+    case 19:
+      if (epi == EPI_SWIGLU) return launch_mfma_ks_s<19, 10>(a, epi, norm, slices, ctr, slots, s);
+      return launch_mfma_ks_s<19, 19>(a, epi, norm, slices, ctr, slots, s);
+    case 8: return launch_mfma_ks_s<8, 8>(a, epi, norm, slices, ctr, slots, s);
+    case 4: return launch_mfma_ks_s<4, 4>(a, epi, norm, slices, ctr, slots, s);
+    default: return KO_ENOTSUP;
+  }
+}
+
+
+}  // namespace
+
+namespace ko {
+
+int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s) {
+  return launch_mfma(a, epi, norm, per_cu, s);
+}
+
+int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
+                   hipStream_t s) {
+  return launch_mfma_ks(a, epi, norm, slices, ctr, slots, s);
+}
+
+}  // namespace ko
