@@ -217,6 +217,29 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
             float* part, long long part_len, int M, int N, int K, int epi, int norm,
             int accumulate, int layout, int rows, int waves, float eps, void* stream);
 
+/* The decode step's tail in one call: the LM head GEMV with the greedy argmax
+ * (ko_gemv with epi 4, ARGMAX, and a NORM prologue when nw != NULL), followed
+ * by the step's bookkeeping. Replaces engine/engine.py:290-292 (the LM head
+ * GEMV, torch.argmax into ids, pos += 1) together with the per-token
+ * device-to-host copy of ids into pinned memory (engine.py:437,516).
+ * logits (bf16 [M, N]) may be NULL; ids [M] int64; pos [M] int32 is advanced.
+ * next_emb/next_h: the next step's embedding gather, as for ko_gemv.
+ * rope (optional, [M][2][head_dim] bf16, 16-byte aligned): receives the cos and
+ * sin rows of cos/sin [max_pos, head_dim] at the advanced position (clamped to
+ * [0, max_pos)), the rows ko_decode_attn_qkv(_oproj) take as `rope` in the
+ * next step (what ko_rope_rows writes).
+ * ring (optional, [ring_rows, M] int64 in pinned host memory): row
+ * ring_ctr[m] (int32 on the device, in [0, ring_rows)) receives ids[m] with a
+ * system-scope store and ring_ctr[m] advances by one, wrapping to 0; a host
+ * that waits for the stream then reads the ids without a copy.
+ * Layouts, scratch (part) and the other arguments as for ko_gemv. */
+int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float* ss, void* logits,
+                      long long* ids, int* pos, const void* next_emb, void* next_h,
+                      const void* cos, const void* sin, int max_pos, int head_dim, void* rope,
+                      long long* ring, int ring_rows, int* ring_ctr, float* part,
+                      long long part_len, int M, int N, int K, int layout, int rows, int waves,
+                      float eps, void* stream);
+
 /* Number of fp32 scratch elements ko_gemv needs for N columns with this launch
  * configuration: the ARGMAX partials (epi 4) of layouts 0-2, or layout 3's
  * slots and counters (rows > 1). A size, not a status; -1 for bad arguments.

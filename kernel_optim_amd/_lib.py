@@ -43,6 +43,10 @@ SIGNATURES = {
     "ko_gemv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                 _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _ll, _int, _int, _int, _int,
                 _int, _int, _int, _int, _int, _f, _c_void_p],
+    "ko_lm_head_argmax": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int,
+                          _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _ll, _int, _int, _int,
+                          _int, _int, _int, _f, _c_void_p],
     "ko_gemv_argmax_scratch": [_int, _int, _int, _int],
     "ko_gemv_tile": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
     "ko_argmax_rows": [_c_void_p, _ll, _int, _int, _c_void_p, _c_void_p],
@@ -97,6 +101,28 @@ def call(name, *args):
 def ptr(t):
     """Device pointer of a tensor (None -> NULL)."""
     return None if t is None else t.data_ptr()
+
+
+_hip = None
+
+
+def host_device_ptr(t):
+    """The device address of a pinned host tensor (hipHostGetDevicePointer), for
+    kernels that store into host memory. Raises if the memory is not mapped
+    pinned memory (a kernel store through it would fault)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(_c_void_p), _c_void_p,
+                                                 ctypes.c_uint]
+        _hip.hipHostGetDevicePointer.restype = _int
+    if t.is_cuda or not t.is_pinned():
+        raise ValueError("host_device_ptr needs a pinned CPU tensor")
+    dev = _c_void_p()
+    st = _hip.hipHostGetDevicePointer(ctypes.byref(dev), _c_void_p(t.data_ptr()), 0)
+    if st != 0 or not dev.value:
+        raise RuntimeError(f"hipHostGetDevicePointer failed (status {st})")
+    return dev.value
 
 
 def stream_ptr(device=None):

@@ -70,10 +70,26 @@ __global__ __launch_bounds__(256) void gemv_tile_kernel(const uint16_t* __restri
 }
 
 // One 1024-thread workgroup per row m: argmax over the work units' (value,
-// index) pairs with the lowest index on ties. Optionally pos[m] += 1 (the decode step's position advance,
-// engine.py:292) and h[m] = emb[ids[m]] (the next step's embedding gather,
-// gemv.py:201-211, so the next step needs no gather launch).
+// index) pairs with the lowest index on ties. Optionally pos[m] += 1 (the decode
+// step's position advance, engine.py:292) and h[m] = emb[ids[m]] (the next step's
+// embedding gather, gemv.py:201-211, so the next step needs no gather launch),
+// and the rest of the decode step's tail (StepTail): the RoPE rows of the new
+// position for the next step's attention, and the id written straight into a
+// ring in pinned host memory (no device-to-host copy per token).
 constexpr int FT = 1024;
+
+struct StepTail {
+  // rope[m] = (cos[p], sin[p]) at the advanced position p = clamp(pos[m], 0, max_pos - 1)
+  const uint16_t* cosb;
+  const uint16_t* sinb;
+  int max_pos, d;
+  uint16_t* rope;
+  // ring[slot * ring_ld + m] = ids[m] with slot = ring_ctr[m], then
+  // ring_ctr[m] = (slot + 1) % ring_rows
+  long long* ring;
+  int ring_rows, ring_ld;
+  int* ring_ctr;
+};
 __device__ __forceinline__ void better(float v, int i, float& bv, int& bi) {
   if (v > bv || (v == bv && i < bi)) {
     bv = v;
@@ -109,9 +125,9 @@ constexpr int FL = 24;
 __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
     const float2* __restrict__ part, int nparts, long long* __restrict__ ids,
     int* __restrict__ pos, const uint16_t* __restrict__ emb, uint16_t* __restrict__ h, int H,
-    int V) {
+    int V, StepTail tail) {
   __shared__ float2 s_best[FT / 64];
-  __shared__ int s_id;
+  __shared__ int s_id, s_pos;
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const float2* pr = part + (long long)m * nparts;
   float bv = -INFINITY;
@@ -148,15 +164,37 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
     int i = __float_as_int(b.y);
     for (int w = 1; w < FT / 64; ++w) better(s_best[w].x, __float_as_int(s_best[w].y), v, i);
     ids[m] = i;
-    if (pos) pos[m] += 1;
+    int p = 0;
+    if (pos) {
+      p = pos[m] + 1;
+      pos[m] = p;
+    }
     s_id = i;
+    s_pos = p;
+    if (tail.ring) {
+      // rows of the ring live in pinned host memory: a system-scope store
+      const int c = tail.ring_ctr[m];
+      const int slot = c >= 0 && c < tail.ring_rows ? c : 0;
+      __hip_atomic_store(tail.ring + (long long)slot * tail.ring_ld + m, (long long)i,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      tail.ring_ctr[m] = slot + 1 < tail.ring_rows ? slot + 1 : 0;
+    }
   }
+  if (emb || tail.rope) __syncthreads();
   if (emb) {
-    __syncthreads();
     const long long tok = s_id;
     if (tok >= 0 && tok < V) {
       for (int c = t; c < (H >> 3); c += FT)
         *reinterpret_cast<uint4*>(h + (long long)m * H + 8 * c) = ldg16(emb + tok * H + 8 * c);
+    }
+  }
+  if (tail.rope) {
+    const int p = min(max(s_pos, 0), tail.max_pos - 1);
+    const int chunks = tail.d >> 3;
+    for (int c = t; c < 2 * chunks; c += FT) {
+      const uint16_t* src = (c < chunks ? tail.cosb : tail.sinb) + (long long)p * tail.d +
+                            8 * (c < chunks ? c : c - chunks);
+      *reinterpret_cast<uint4*>(tail.rope + (long long)m * 2 * tail.d + 8 * c) = ldg16(src);
     }
   }
 }
@@ -230,14 +268,11 @@ long long parts_for(int N, int layout, int rows, int waves) {
   return ((units + waves - 1) / waves) * waves;
 }
 
-}  // namespace
-
-extern "C" {
-
-int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
-            float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
-            float* part, long long part_len, int M, int N, int K, int epi, int norm,
-            int accumulate, int layout, int rows, int waves, float eps, void* stream) {
+int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
+              float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
+              float* part, long long part_len, int M, int N, int K, int epi, int norm,
+              int accumulate, int layout, int rows, int waves, float eps, const StepTail& tail,
+              hipStream_t s) {
   if (!x || !w || M < 1 || N < 1 || K < 8 || (K & 7)) return KO_EINVAL;
   if (epi < EPI_F32 || epi > EPI_ARGMAX) return KO_EINVAL;
   if (!al16(x) || !al16(w)) return KO_EINVAL;
@@ -269,7 +304,6 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
     if ((next_emb == nullptr) != (next_h == nullptr)) return KO_EINVAL;
     if (next_emb && (!al16(next_emb) || !al16(next_h))) return KO_EINVAL;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
   for (int m0 = 0; m0 < M; m0 += mstep) {
     GemvArgs a;
     const int mr = M - m0 < mstep ? M - m0 : mstep;
@@ -303,16 +337,64 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
                           part + ((N + 15) / 16 + 63) / 64 * 64, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
+      StepTail tl = tail;
+      if (tl.rope) tl.rope += (long long)m0 * 2 * tl.d;
+      if (tl.ring) {
+        tl.ring += m0;
+        tl.ring_ctr += m0;
+      }
       hipLaunchKernelGGL(argmax_finalize_kernel, dim3(mr), dim3(FT), 0, s, a.part, a.nparts,
                          ids + m0, pos_inc ? pos_inc + m0 : nullptr,
                          static_cast<const uint16_t*>(next_emb),
                          next_h ? static_cast<uint16_t*>(next_h) + (long long)m0 * K : nullptr, K,
-                         N);
+                         N, tl);
       st = KO_LAUNCH_STATUS();
       if (st) return st;
     }
   }
   return KO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
+            float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
+            float* part, long long part_len, int M, int N, int K, int epi, int norm,
+            int accumulate, int layout, int rows, int waves, float eps, void* stream) {
+  const StepTail none = {};
+  return gemv_impl(x, w, y, nw, ss, h, ss_out, ids, pos_inc, next_emb, next_h, part, part_len, M,
+                   N, K, epi, norm, accumulate, layout, rows, waves, eps, none,
+                   static_cast<hipStream_t>(stream));
+}
+
+int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float* ss, void* logits,
+                      long long* ids, int* pos, const void* next_emb, void* next_h,
+                      const void* cos, const void* sin, int max_pos, int head_dim, void* rope,
+                      long long* ring, int ring_rows, int* ring_ctr, float* part,
+                      long long part_len, int M, int N, int K, int layout, int rows, int waves,
+                      float eps, void* stream) {
+  StepTail tail = {};
+  if (rope) {
+    if (!pos || !cos || !sin || max_pos < 1 || head_dim < 8 || (head_dim & 7)) return KO_EINVAL;
+    if (!al16(cos) || !al16(sin) || !al16(rope)) return KO_EINVAL;
+    tail.cosb = static_cast<const uint16_t*>(cos);
+    tail.sinb = static_cast<const uint16_t*>(sin);
+    tail.max_pos = max_pos;
+    tail.d = head_dim;
+    tail.rope = static_cast<uint16_t*>(rope);
+  }
+  if (ring) {
+    if (!ring_ctr || ring_rows < 1) return KO_EINVAL;
+    tail.ring = ring;
+    tail.ring_rows = ring_rows;
+    tail.ring_ld = M;
+    tail.ring_ctr = ring_ctr;
+  }
+  return gemv_impl(x, w, logits, nw, ss, nullptr, nullptr, ids, pos, next_emb, next_h, part,
+                   part_len, M, N, K, EPI_ARGMAX, nw != nullptr, 0, layout, rows, waves, eps,
+                   tail, static_cast<hipStream_t>(stream));
 }
 
 int ko_gemv_tile(const void* w, void* wt, int rows, int K, void* stream) {

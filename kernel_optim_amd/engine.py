@@ -295,7 +295,10 @@ class Engine:
         self.rope = torch.zeros(B, 2, cfg.head_dim, dtype=bf, device=dev)
         self.logits = (torch.zeros(B, cfg.vocab, dtype=bf, device=dev) if self.keep_logits
                        else None)
+        # ids of step j land in row j: the prefill's by a copy, the decode steps'
+        # straight from the LM head's tail (ring_ctr: the next row it writes)
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
+        self.ring_ctr = torch.zeros(B, dtype=torch.int32, device=dev)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
                                     unit=ATTN_UNIT or None, fused_combine=True)
@@ -388,12 +391,21 @@ class Engine:
         _log(f"B={B} K={self.K}: step {t1 * 1e3:.0f}us verify {tk * 1e3:.0f}us -> speculate "
              f"while >= {self.breakeven:.3f} tokens/step")
 
+    def _set_pos(self, p):
+        """Set the positions (an int or a [B] tensor) and the RoPE rows the next
+        one-token step reads for them (the step itself then keeps both current)."""
+        if isinstance(p, torch.Tensor):
+            self.pos.copy_(p, non_blocking=True)
+        else:
+            self.pos.fill_(p)
+        rope_rows(self.pos, self._cos, self._sin, self.rope)
+
     def _time_graph(self, g, reps=10):
         """Mean replay time (ms) of a captured step from positions where every
         cache write stays inside the capacity."""
         start = max(0, min(self.S, self.cap - (reps + 2) - (self.K + 1)))
         torch.cuda.synchronize()
-        self.pos.fill_(start)
+        self._set_pos(start)
         g.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -415,15 +427,19 @@ class Engine:
         """One decode token per sequence at pos[b]; greedy ids; positions advance."""
         cfg = self.cfg
         g, W = self.gv, self.gw  # W: each projection's weights in its launch layout
-        h = self.h   # holds embed[ids]: written by the previous step's LM head (or prefill)
+        # h holds embed[ids] and rope the RoPE rows at pos: both written by the
+        # previous step's LM head tail (or by the prefill hand-off)
+        h = self.h
         fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
-        rope_rows(self.pos, self._cos, self._sin, self.rope)  # the step's RoPE rows, once
         for i, lw in enumerate(self.w["layers"]):
             decode_layer(g, W, i, lw, self.attn, h, self.qkv, self.attn_out, self.act,
                          self.k_cache[i], self.v_cache[i], self._cos, self._sin, self.pos,
                          self.rope, cfg.eps, fuse_o)
+        # LM head + greedy ids + pos += 1 + the next step's embedding rows and RoPE
+        # rows + the ids into the pinned host ring, in one call
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
-                pos_inc=self.pos, next_emb=self.w["embed"], next_h=h)
+                pos_inc=self.pos, next_emb=self.w["embed"], next_h=h,
+                rope=(self._cos, self._sin, self.rope), ring=(self.pin_ids, self.ring_ctr))
 
     def _step1_mm(self):
         """One decode token per sequence with hipBLASLt GEMMs (torch.mm) between
@@ -503,7 +519,7 @@ class Engine:
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        self.pos.zero_()
+        self._set_pos(0)
         with torch.cuda.graph(g):
             fn()
         torch.cuda.synchronize()
@@ -514,7 +530,7 @@ class Engine:
         ids, logits = prefill(self.cfg, self.w, prompt, self.k_cache, self.v_cache, self._cos,
                               self._sin)
         self.ids.copy_(ids)
-        self.pos.fill_(prompt.shape[1])
+        self._set_pos(prompt.shape[1])
         embed_ss(self.ids, self.w["embed"], self.h, None)   # the first decode step's input
         if self.logits is not None:
             self.logits.copy_(logits)
@@ -534,7 +550,7 @@ class Engine:
             raise ValueError("verify_step needs an engine set up with speculation (spec=True, "
                              "max_new_tokens > 2, a batch of at most 32)")
         self.vin.copy_(torch.as_tensor(rows, dtype=torch.int64))
-        self.pos.copy_(torch.as_tensor(pos, dtype=torch.int32))
+        self._set_pos(torch.as_tensor(pos, dtype=torch.int32).to(DEVICE))
         self.gk.replay()
         torch.cuda.synchronize()
         return self.vout.cpu(), (self.logitsT.cpu() if self.keep_logits else None)
@@ -543,7 +559,7 @@ class Engine:
     def time_step(self, reps=20):
         """Mean GPU time (ms) of one replayed decode step, from positions S."""
         torch.cuda.synchronize()
-        self.pos.fill_(self.S)
+        self._set_pos(self.S)
         self.g1.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -571,17 +587,24 @@ class Engine:
         if self.K:
             yield from self._generate_spec(input_ids, N, stream)
             return
+        # The fused step writes its ids into row ring_ctr of ids_h itself; the
+        # hipBLASLt step's ids are copied after each replay.
+        ring = self.step_kind == "fused"
+        if ring:
+            self.ring_ctr.fill_(1)
         # Keep one replay in flight: queue step j before waiting for step j-1.
         if N > 1:
             self.g1.replay()
-            ids_h[1].copy_(self.ids, non_blocking=True)
+            if not ring:
+                ids_h[1].copy_(self.ids, non_blocking=True)
             ev[1].record(stream)
         ev[0].synchronize()
         yield ids_h[0].tolist()
         for j in range(1, N):
             if j + 1 < N:
                 self.g1.replay()
-                ids_h[j + 1].copy_(self.ids, non_blocking=True)
+                if not ring:
+                    ids_h[j + 1].copy_(self.ids, non_blocking=True)
                 ev[j + 1].record(stream)
             ev[j].synchronize()
             if j == N - 1:
@@ -644,13 +667,17 @@ class Engine:
             ids_h[0, b] = outs[b][-1]
             pos_h[b] = S + len(outs[b]) - 1
         self.ids.copy_(ids_h[0], non_blocking=True)
-        self.pos.copy_(pos_h, non_blocking=True)
+        self._set_pos(pos_h)
         embed_ss(self.ids, self.w["embed"], self.h, None)   # the step's input rows
         todo = N - min(len(o) for o in outs)
+        ring = self.step_kind == "fused"
+        if ring:
+            self.ring_ctr.fill_(1)
         # pipelined: step j is queued before the host waits for step j-1
         for j in range(1, todo + 1):
             self.g1.replay()
-            ids_h[j].copy_(self.ids, non_blocking=True)
+            if not ring:
+                ids_h[j].copy_(self.ids, non_blocking=True)
             ev[j].record(stream)
             if j > 1:
                 emitted = yield from self._drain(j - 1, outs, N, emitted)

@@ -135,10 +135,15 @@ class Gemv:
                 self._tiles[id(w)] = (weakref.ref(w), t)
 
     def __call__(self, x, w, y=None, nw=None, ss=None, h=None, ss_out=None, cfg=None, ids=None,
-                 pos_inc=None, next_emb=None, next_h=None):
+                 pos_inc=None, next_emb=None, next_h=None, rope=None, ring=None):
         """ARGMAX extras: ``pos_inc`` ([M] int32) is advanced by one; with
         ``next_emb`` ([N, K] bf16, the embedding) the chosen ids' rows are gathered
-        into ``next_h`` ([M, K] bf16), the next decode step's input."""
+        into ``next_h`` ([M, K] bf16), the next decode step's input. The decode
+        step's tail (ko_lm_head_argmax): ``rope = (cos, sin, out)`` writes the
+        RoPE rows of the advanced positions into out ([M, 2, d] bf16, what
+        rope_rows writes), and ``ring = (host, ctr)`` stores the ids into row
+        ctr[m] of host ([R, M] int64, pinned) and advances ctr ([M] int32 on the
+        device) modulo R."""
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
@@ -167,8 +172,37 @@ class Gemv:
             if next_emb is not None:
                 _check(next_emb, "next_emb", BF16, (N, K))
                 _check(next_h, "next_h", BF16, (M, K))
+            if rope is not None:
+                cos, sin, rope_out = rope
+                _need(pos_inc is not None, "rope rows need the positions (pos_inc)")
+                _check(cos, "cos", BF16)
+                _need(cos.dim() == 2 and tuple(sin.shape) == tuple(cos.shape),
+                      "cos/sin must be [rows, d]")
+                _check(sin, "sin", BF16)
+                _check(rope_out, "rope", BF16, (M, 2, cos.shape[1]))
+            if ring is not None:
+                host, ctr = ring
+                _need(isinstance(host, torch.Tensor) and host.dtype == torch.int64
+                      and not host.is_cuda and host.is_pinned() and host.is_contiguous()
+                      and host.dim() == 2 and host.shape[1] == M,
+                      "ring host must be a pinned contiguous int64 [R, M] CPU tensor")
+                _check(ctr, "ring counter", torch.int32, (M,))
         part = (self._scratch(x.device, (layout, rows, waves))
                 if epi == EPI_ARGMAX or (layout == 3 and rows > 1) else None)
+        if epi == EPI_ARGMAX and (rope is not None or ring is not None):
+            cos, sin, rope_out = rope if rope is not None else (None, None, None)
+            host, ctr = ring if ring is not None else (None, None)
+            _lib.call("ko_lm_head_argmax", _lib.ptr(x), _lib.ptr(w),
+                      _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
+                      _lib.ptr(y), _lib.ptr(ids), _lib.ptr(pos_inc), _lib.ptr(next_emb),
+                      _lib.ptr(next_h), _lib.ptr(cos), _lib.ptr(sin),
+                      0 if cos is None else cos.shape[0], 0 if cos is None else cos.shape[1],
+                      _lib.ptr(rope_out),
+                      None if host is None else _lib.host_device_ptr(host),
+                      0 if host is None else host.shape[0],
+                      _lib.ptr(ctr), _lib.ptr(part), part.numel(), M, N, K, layout, rows, waves,
+                      self.eps, _lib.stream_ptr())
+            return
         _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
                   _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
                   _lib.ptr(h), _lib.ptr(ss_out), _lib.ptr(ids), _lib.ptr(pos_inc),

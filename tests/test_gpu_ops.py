@@ -313,6 +313,75 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
         assert torch.equal(ids2, ids)
 
 
+@pytest.mark.parametrize("M,cfg", [(1, (0, 8, 0)), (2, (1, 2, 4)), (4, (0, 4, 0)),
+                                   (16, (2, 1, 0)), (20, (0, 8, 0))])
+def test_lm_head_step_tail(dev, M, cfg):
+    """ko_lm_head_argmax: the LM head with the decode step's tail. The ids, logits,
+    position advance and embedding gather equal ko_gemv's ARGMAX epilogue; the
+    RoPE rows of the advanced positions equal rope_rows (and the table rows, the
+    last position clamped to the table); the ids land in the pinned host ring at
+    row ring_ctr[m], which advances and wraps, on eager calls and graph replays
+    (M = 20 runs as two launch slices of 16 and 4 rows)."""
+    fused, gemv = K()
+    V, H, d, rows = 151936, 2560, 128, 40
+    g = _g(dev, 50)
+    E = _weights(dev, V, H, 51)
+    x = torch.randn(M, H, device=dev, generator=g).to(BF)
+    nw = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(BF)
+    op = gemv.Gemv(M, V, H, gemv.EPI_ARGMAX, norm=True)
+    op.cfg = cfg
+    Ew = gemv.tile_weights(E) if cfg[0] == 2 else E
+    cos, sin = (t.to(dev) for t in O.rope_tables(rows, d))
+    pos0 = torch.arange(M, dtype=torch.int32) * 2 + 5
+    pos0[-1] = rows - 1          # advances past the table: the rows clamp to the last
+    # the plain ARGMAX epilogue, then the step tail's separate pieces
+    ids_a = torch.empty(M, device=dev, dtype=torch.int64)
+    lg_a = torch.empty(M, V, device=dev, dtype=BF)
+    pos_a = pos0.to(dev)
+    nxt_a = torch.zeros(M, H, device=dev, dtype=BF)
+    op(x, Ew, y=lg_a, nw=nw, ids=ids_a, pos_inc=pos_a, next_emb=E, next_h=nxt_a)
+    rope_a = torch.empty(M, 2, d, device=dev, dtype=BF)
+    fused.rope_rows(pos_a, cos, sin, rope_a)
+    # the tail in one call
+    R = 3
+    ring = torch.full((R, M), -1, dtype=torch.int64, pin_memory=True)
+    ctr = torch.ones(M, dtype=torch.int32, device=dev)
+    ids_b = torch.empty(M, device=dev, dtype=torch.int64)
+    lg_b = torch.empty(M, V, device=dev, dtype=BF)
+    pos_b = pos0.to(dev)
+    nxt_b = torch.zeros(M, H, device=dev, dtype=BF)
+    rope_b = torch.zeros(M, 2, d, device=dev, dtype=BF)
+    kw = dict(y=lg_b, nw=nw, ids=ids_b, pos_inc=pos_b, next_emb=E, next_h=nxt_b,
+              rope=(cos, sin, rope_b), ring=(ring, ctr))
+    op(x, Ew, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(ids_b, ids_a) and torch.equal(lg_b, lg_a) and torch.equal(nxt_b, nxt_a)
+    assert torch.equal(pos_b, pos_a)
+    assert torch.equal(rope_b, rope_a)
+    p = pos_a.cpu().long().clamp(0, rows - 1)
+    assert torch.equal(rope_b[:, 0].cpu(), cos.cpu()[p]) and torch.equal(rope_b[:, 1].cpu(), sin.cpu()[p])
+    assert torch.equal(ring[1], ids_a.cpu()) and torch.equal(ring[0], torch.full((M,), -1))
+    assert torch.equal(ctr.cpu(), torch.full((M,), 2, dtype=torch.int32))
+    # graph replays: rows 2, then 0 (wrapped), then 1
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op(x, Ew, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    ring.fill_(-1)
+    ctr.fill_(2)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        op(x, Ew, **kw)
+    for want_row, want_ctr in ((2, 0), (0, 1), (1, 2)):
+        ring[want_row].fill_(-1)
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ring[want_row], ids_a.cpu()), want_row
+        assert torch.equal(ctr.cpu(), torch.full((M,), want_ctr, dtype=torch.int32))
+
+
 @pytest.mark.parametrize("M,N,ld", [(5, 151936, 151936), (3, 1003, 1008), (80, 4096, 4104)])
 def test_argmax_rows_first_index_and_graph(dev, M, N, ld):
     """ko_argmax_rows against the first-maximum argmax; planted ties (the same
