@@ -233,17 +233,15 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         # o projection in the attention's launch where it fits (B <= 2)
         att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
         att.oproj_delay_ns = 500
-        att.gateup_delay_ns = 1000
         rope = torch.empty(B, 2, cfg.head_dim, device=dev, dtype=torch.bfloat16)
         fuse_o = att.oproj_fusable()
-        fuse_gu = fuse_o and att.oproj_gateup_fusable(cfg.hidden, cfg.inter)
         ops, W = build_decode_gemvs(cfg, B, raw, time.monotonic() + 20, tiled_fn)
 
         def layers():
             rope_rows(pos, cos, sin, rope)
             for i in range(nsets):
                 decode_layer(ops, W, i, L[i], att, h, qkv, att_out, act, kc[i], vc[i], cos, sin,
-                             pos, rope, cfg.eps, fuse_o, fuse_gu)
+                             pos, rope, cfg.eps, fuse_o)
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -270,8 +268,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
                         "gbs": round(nbytes / us / 1e3, 1),
                         "roofline_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
                         "gemv_cfgs": {k: v.cfg for k, v in ops.items() if k in W},
-                        "o_proj": "in the attention launch" if fuse_o else "own launch",
-                        "gate_up": "in the attention launch" if fuse_gu else "own launch"}
+                        "o_proj": "in the attention launch" if fuse_o else "own launch"}
         del kc, vc
         torch.cuda.empty_cache()
     return res

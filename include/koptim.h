@@ -125,34 +125,6 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
 /* int32 elements of ko_decode_attn_qkv_oproj's sync array (a size, not a status). */
 long long ko_decode_attn_qkv_oproj_sync_ints(void);
 
-/* ko_decode_attn_qkv_oproj and the gate/up projection in ONE launch (B <= 2,
- * nq*head_dim = 4096, H = 2560, I % 8 == 0; else KO_ENOTSUP): after the
- * attention (out) and the o projection with its residual add (h), act [B, I]
- * <- bf16(bf16(silu(g)) * u) with (g | u) = RMSNorm(h; w_post, eps) @ w_gu^T,
- * w_gu [2I, H] row-major (gate rows, then up rows), the NORM + SWIGLU GEMV of
- * engine/kernels/gemv.py. Replaces engine/engine.py:279-285 (qk_norm_rope_acc,
- * the attention, the o GEMV with its residual and the gate/up GEMV); the
- * down projection stays a launch of its own. Extra workgroups own 16 gate/up
- * columns each (8 when B = 2): they load their weights as soon as they are
- * resident and wait on a device-coherent count of finished o-projection
- * workgroups, so the weights stream during the attention. sync:
- * ko_decode_attn_oproj_gateup_sync_ints() int32, zero before the first call,
- * left zero by every call; err as for ko_decode_attn_qkv_oproj (either wait
- * giving up sets it); o_delay_ns / gu_delay_ns hold the projections' weight
- * loads back so the attention's first loads go ahead. */
-int ko_decode_attn_oproj_gateup(const void* qkv, const void* q_w, const void* k_w,
-                                const void* cos, const void* sin, int max_pos, const int* pos,
-                                void* k_cache, void* v_cache, int cap, long long cache_b_stride,
-                                long long cache_h_stride, int B, int nkv, int head_dim, int unit,
-                                int max_units, int grid_waves, float eps, float scale,
-                                float* o_part, float* ml, int* counters, void* out,
-                                const void* w_o, void* h, int H, const void* w_gu,
-                                const void* w_post, void* act, int I, int* sync, int* err,
-                                int o_delay_ns, int gu_delay_ns, const void* rope, void* stream);
-
-/* int32 elements of ko_decode_attn_oproj_gateup's sync array (a size, not a status). */
-long long ko_decode_attn_oproj_gateup_sync_ints(void);
-
 /* out[b] = (cos[p], sin[p]), p = clamp(pos[b], 0, rows - 1): each sequence's
  * RoPE rows at its new position for the rope argument above (the rows that
  * qk_norm_rope, engine/kernels/fused.py:71-87, reads). cos/sin [rows, d] bf16,

@@ -56,21 +56,13 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                                  _c_void_p, _int, _c_void_p, _c_void_p],
     "ko_decode_attn_qkv_oproj_sync_ints": [],
-    "ko_decode_attn_oproj_gateup": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int,
-                                    _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll, _int, _int,
-                                    _int, _int, _int, _int, _f, _f, _c_void_p, _c_void_p,
-                                    _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
-                                    _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _int, _int,
-                                    _c_void_p, _c_void_p],
-    "ko_decode_attn_oproj_gateup_sync_ints": [],
     "ko_decode_attn_token_rows": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll,
                                   _int, _int, _int, _int, _int, _int, _int, _f, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p],
 }
 
 # Entry points whose return value is a size, not a status.
-RESTYPES = {"ko_gemv_argmax_scratch": _ll, "ko_decode_attn_qkv_oproj_sync_ints": _ll,
-            "ko_decode_attn_oproj_gateup_sync_ints": _ll}
+RESTYPES = {"ko_gemv_argmax_scratch": _ll, "ko_decode_attn_qkv_oproj_sync_ints": _ll}
 
 _ERRORS = {-22: "invalid argument", -34: "size out of range", -95: "unsupported shape"}
 

@@ -55,9 +55,6 @@ TUNE_BUDGET_S = 60.0
 # attention and the o projection in one launch for 1-2 sequences (ENGINE_FUSE_OPROJ=0: two)
 FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
 OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "500"))
-# ... and the gate/up projection in that launch too (ENGINE_FUSE_GATEUP=0: its own)
-FUSE_GATEUP = os.environ.get("ENGINE_FUSE_GATEUP", "1") == "1"
-GATEUP_DELAY_NS = int(os.environ.get("ENGINE_GATEUP_DELAY_NS", "1000"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 # decode-step graph: "auto" captures the fused-GEMV step and the hipBLASLt step for
@@ -190,22 +187,15 @@ def build_decode_gemvs(cfg, M, raw, deadline, tiled_fn=None, tune=True, log=""):
 
 
 def decode_layer(gv, W, i, lw, attn, h, qkv, attn_out, act, k_cache, v_cache, cos, sin, pos,
-                 rope, eps, fuse_o, fuse_gu=False):
+                 rope, eps, fuse_o):
     """Layer i of the one-token decode step (engine.py:278-287 in this package's
     launches): qkv GEMV (RMSNorm prologue) -> attention (q/k norm + RoPE + KV
     append at pos, split-K partials, last-unit merge), with the o projection and
     its residual add in the same launch when ``fuse_o`` -> o GEMV (+ residual)
-    otherwise -> gate/up GEMV (RMSNorm prologue, SwiGLU), in the attention's
-    launch too when ``fuse_gu`` -> down GEMV (+ residual).
+    otherwise -> gate/up GEMV (RMSNorm prologue, SwiGLU) -> down GEMV (+ residual).
     h [B, H] is the residual stream, updated in place; k_cache/v_cache are the
     layer's [B, nkv, cap, d] slices; rope the step's RoPE rows (rope_rows)."""
     gv["qkv"](h, W["qkv"][i], y=qkv, nw=lw["w_in"])
-    if fuse_gu:  # attention + o projection + residual + gate/up + SwiGLU in one launch
-        attn.decode_qkv_oproj_gateup(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, k_cache,
-                                     v_cache, attn_out, eps, lw["o"], h, lw["gu"], lw["w_post"],
-                                     act, rope=rope)
-        gv["down"](act, W["down"][i], h=h)
-        return
     if fuse_o:
         attn.decode_qkv_oproj(qkv, lw["q_norm"], lw["k_norm"], cos, sin, pos, k_cache, v_cache,
                               attn_out, eps, lw["o"], h, rope=rope)
@@ -313,7 +303,6 @@ class Engine:
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
                                     unit=ATTN_UNIT or None, fused_combine=True)
         self.attn.oproj_delay_ns = OPROJ_DELAY_NS
-        self.attn.gateup_delay_ns = GATEUP_DELAY_NS
         L = self.w["layers"]
         raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],
                    down=[l["down"] for l in L], lm=[self.w["lm_head"]])
@@ -442,11 +431,10 @@ class Engine:
         # previous step's LM head tail (or by the prefill hand-off)
         h = self.h
         fuse_o = FUSE_OPROJ and self.attn.oproj_fusable()
-        fuse_gu = fuse_o and FUSE_GATEUP and self.attn.oproj_gateup_fusable(cfg.hidden, cfg.inter)
         for i, lw in enumerate(self.w["layers"]):
             decode_layer(g, W, i, lw, self.attn, h, self.qkv, self.attn_out, self.act,
                          self.k_cache[i], self.v_cache[i], self._cos, self._sin, self.pos,
-                         self.rope, cfg.eps, fuse_o, fuse_gu)
+                         self.rope, cfg.eps, fuse_o)
         # LM head + greedy ids + pos += 1 + the next step's embedding rows and RoPE
         # rows + the ids into the pinned host ring, in one call
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,

@@ -114,14 +114,11 @@ class DecodeAttention:
         # them at zero
         self.counters = (torch.zeros(rows_k * nkv, dtype=torch.int32, device=device)
                          if fused_combine else None)
-        # decode_qkv_oproj(_gateup): their counters and done flags, and their
-        # wait-failure flag
-        n_sync = max(_lib.lib().ko_decode_attn_qkv_oproj_sync_ints(),
-                     _lib.lib().ko_decode_attn_oproj_gateup_sync_ints())
-        self.sync = torch.zeros(n_sync, dtype=torch.int32, device=device)
+        # decode_qkv_oproj: its counters and done flags, and its wait-failure flag
+        self.sync = torch.zeros(_lib.lib().ko_decode_attn_qkv_oproj_sync_ints(), dtype=torch.int32,
+                                device=device)
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
         self.oproj_delay_ns = 1000
-        self.gateup_delay_ns = 1000
         self.scale = d ** -0.5
 
     def _check_kv(self, k_cache, v_cache, lens):
@@ -223,51 +220,6 @@ class DecodeAttention:
                   _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters), _lib.ptr(out),
                   _lib.ptr(w_o), _lib.ptr(h), H, _lib.ptr(self.sync), _lib.ptr(self.err),
                   self.oproj_delay_ns, _lib.ptr(rope), _lib.stream_ptr())
-
-    def oproj_gateup_fusable(self, H, I):
-        """decode_qkv_oproj_gateup serves what decode_qkv_oproj serves with the
-        o projection's input width nq * d = 4096 and hidden size H = 2560
-        (attn_mlp.hip, ko_decode_attn_oproj_gateup)."""
-        return self.oproj_fusable() and self.nq * self.d == 4096 and H == 2560 and I % 8 == 0
-
-    def decode_qkv_oproj_gateup(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps,
-                                w_o, h, w_gu, w_post, act, rope=None):
-        """decode_qkv_oproj and then the gate/up projection in the same launch:
-        act <- bf16(bf16(silu(g)) * u) with (g | u) = RMSNorm(h; w_post) @ w_gu^T
-        (the NORM + SWIGLU GEMV of engine.py:284), read from the h the o
-        projection has just updated. w_gu: [2I, H] row-major (gate | up) bf16;
-        w_post: [H]; act: [B, I]. The gate/up weights stream while the attention
-        runs."""
-        B, nq, nkv, d = self.B, self.nq, self.nkv, self.d
-        _need(h.dim() == 2 and h.shape[0] == B, "h must be [B, H]")
-        H = h.shape[1]
-        _need(act.dim() == 2 and act.shape[0] == B, "act must be [B, I]")
-        I = act.shape[1]
-        _need(self.oproj_gateup_fusable(H, I), "decode_qkv_oproj_gateup needs B <= 2, "
-              "fused_combine, a unit of 4 wavefronts, nq * d = 4096 and H = 2560")
-        _check(qkv, "qkv", BF16, (B, (nq + 2 * nkv) * d))
-        _check(out, "out", BF16, (B, nq * d))
-        _check(q_w, "q_w", BF16, (d,))
-        _check(k_w, "k_w", BF16, (d,))
-        _check(cos, "cos", BF16)
-        _check(sin, "sin", BF16)
-        _need(cos.dim() == 2 and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape),
-              "cos/sin must be [rows, d]")
-        _check(h, "h", BF16, (B, H))
-        _check(w_o, "w_o", BF16, (H, nq * d))
-        _check(w_gu, "w_gu", BF16, (2 * I, H))
-        _check(w_post, "w_post", BF16, (H,))
-        _check(act, "act", BF16, (B, I))
-        self._check_kv(k_cache, v_cache, pos)
-        self._check_rope(rope)
-        _lib.call("ko_decode_attn_oproj_gateup", _lib.ptr(qkv), _lib.ptr(q_w), _lib.ptr(k_w),
-                  _lib.ptr(cos), _lib.ptr(sin), cos.shape[0], _lib.ptr(pos), _lib.ptr(k_cache),
-                  _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
-                  self.unit, self.max_units, self.grid_waves, eps, self.scale,
-                  _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters), _lib.ptr(out),
-                  _lib.ptr(w_o), _lib.ptr(h), H, _lib.ptr(w_gu), _lib.ptr(w_post), _lib.ptr(act), I,
-                  _lib.ptr(self.sync), _lib.ptr(self.err), self.oproj_delay_ns,
-                  self.gateup_delay_ns, _lib.ptr(rope), _lib.stream_ptr())
 
     def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, rope=None):
         """Decode step (T=1) straight from the bf16 QKV projection [B, (nq+2nkv)*d]:

@@ -406,90 +406,3 @@ def test_decode_qkv_oproj_equals_attention_then_o_gemv(dev, B, cap, pos0):
     got = run(True, 4)
     for name, a, b in zip(("out", "h", "k", "v"), got, want):
         assert torch.equal(a, b), name
-
-
-@pytest.mark.parametrize("B,cap,pos0", [(1, 1296, 1024), (1, 1296, 0), (2, 640, 517)])
-def test_decode_qkv_oproj_gateup(dev, B, cap, pos0):
-    """Attention + o projection + gate/up projection in one launch
-    (ko_decode_attn_oproj_gateup, the engine's batch-1/2 layer body):
-    - the attention output and the KV append are bit-equal to decode_qkv_oproj's;
-    - h is the RESID GEMV of the launch's own attention output (oracle, 1 bf16 ulp);
-    - act is the NORM + SWIGLU GEMV of the launch's own h (oracle, 1 bf16 ulp);
-    - over graph replays whose positions advance, the launch re-arms its counters
-      and flags, never times out, and every replay matches an eager run of the
-      same steps bit for bit."""
-    from oracle import ops as O
-    from tests.bf16util import assert_bf16_close, one_ulp_at
-    fused_mod = _fused()
-    nq, nkv, d, H, I = 32, 8, 128, 2560, 9728
-    g = torch.Generator(device=dev).manual_seed(70 + B)
-    bf = torch.bfloat16
-    qkv = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g).to(bf)
-    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(bf)
-    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(bf)
-    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
-    k0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(bf)
-    v0 = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(bf)
-    w_o = (0.02 * torch.randn(H, nq * d, device=dev, generator=g)).to(bf)
-    w_gu = (0.02 * torch.randn(2 * I, H, device=dev, generator=g)).to(bf)
-    w_post = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(bf)
-    h0 = torch.randn(B, H, device=dev, generator=g).to(bf)
-    pos_start = torch.tensor([pos0, max(pos0 - 300, 0)][:B], dtype=torch.int32, device=dev)
-
-    def state():
-        return dict(k=k0.clone(), v=v0.clone(), h=h0.clone(), pos=pos_start.clone(),
-                    out=torch.zeros(B, nq * d, device=dev, dtype=bf),
-                    act=torch.zeros(B, I, device=dev, dtype=bf),
-                    rope=torch.zeros(B, 2, d, device=dev, dtype=bf))
-
-    att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, fused_combine=True)
-    assert att.oproj_gateup_fusable(H, I)
-
-    def step(st, gateup=True):
-        fused_mod.rope_rows(st["pos"], cos, sin, st["rope"])
-        if gateup:
-            att.decode_qkv_oproj_gateup(qkv, qw, kw, cos, sin, st["pos"], st["k"], st["v"],
-                                        st["out"], 1e-6, w_o, st["h"], w_gu, w_post, st["act"],
-                                        rope=st["rope"])
-        else:
-            att.decode_qkv_oproj(qkv, qw, kw, cos, sin, st["pos"], st["k"], st["v"], st["out"],
-                                 1e-6, w_o, st["h"], rope=st["rope"])
-        st["pos"].add_(1)
-
-    # one eager step of each, from the same inputs
-    a, b = state(), state()
-    step(a)
-    step(b, gateup=False)
-    torch.cuda.synchronize()
-    att.check_sync()
-    for name in ("out", "k", "v"):
-        assert torch.equal(a[name], b[name]), name
-    h_ref, _ = O.gemv(a["out"].cpu(), w_o.cpu(), O.EPI_RESID, h=h0.cpu())
-    assert_bf16_close(a["h"].cpu(), h_ref, max_frac=0.02)
-    hf = a["h"].cpu().float()
-    act_ref = O.gemv(a["h"].cpu(), w_gu.cpu(), O.EPI_SWIGLU, nw=w_post.cpu(), ss=(hf * hf).sum(-1))
-    assert_bf16_close(a["act"].cpu(), act_ref, max_frac=0.02, atol=one_ulp_at(act_ref))
-
-    # eager steps against graph replays of the same steps
-    steps = 4
-    e = state()
-    for _ in range(steps):
-        step(e)
-    torch.cuda.synchronize()
-    r = state()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step(r)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step(r)
-    for _ in range(steps - 1):
-        graph.replay()
-    torch.cuda.synchronize()
-    assert torch.all(att.counters == 0) and torch.all(att.sync == 0)
-    att.check_sync()
-    for name in ("out", "h", "act", "k", "v", "pos"):
-        assert torch.equal(r[name], e[name]), name

@@ -59,9 +59,8 @@ def test_decoder_layer_2048_cached_keys(dev, B):
     attn_out = torch.zeros(B, nq * d, dtype=torch.bfloat16, device=dev)
     act = torch.zeros(B, cfg.inter, dtype=torch.bfloat16, device=dev)
     fuse_o = attn.oproj_fusable()
-    fuse_gu = fuse_o and attn.oproj_gateup_fusable(cfg.hidden, cfg.inter)
     decode_layer(gv, W, 0, lw, attn, h, qkv, attn_out, act, k_cache, v_cache, cos, sin, pos,
-                 rope, cfg.eps, fuse_o, fuse_gu)
+                 rope, cfg.eps, fuse_o)
     torch.cuda.synchronize()
     attn.check_sync()
 
@@ -85,8 +84,7 @@ def test_decoder_layer_2048_cached_keys(dev, B):
     got_h = h.float().cpu()
     err = float((got_h - want_h).abs().max())
     print(f"layer B={B} at {CTX} cached keys (o projection "
-          f"{'in the attention launch' if fuse_o else 'own launch'}, gate/up "
-          f"{'in the attention launch' if fuse_gu else 'own launch'}, cfgs "
+          f"{'in the attention launch' if fuse_o else 'own launch'}, cfgs "
           f"{ {k: gv[k].cfg for k in W} }): max |dh| {err:.3e}, max |h| "
           f"{float(want_h.abs().max()):.3f}")
     # the residual stream is rounded to bf16 at the scale of its largest elements
