@@ -10,11 +10,15 @@ one. Inputs are resident in HBM before the timed region starts.
 
 Prints one JSON line: value = algorithmic HBM GB/s (K+V of every valid key +
 q + out) over the timed steps; ``roofline`` for the dominant kernel
-(attn_partial_kernel) timed with HIP events on its launch stream;
-``cpu_baseline`` = the CPU oracle on a bounded sample of the same workload.
+(the split-K partial kernel) timed with HIP events on its launch stream;
+``cpu_baseline`` = the reference's CPU path (torch SDPA in bf16, as
+Transformers' sdpa attention runs it) on the same workload, timed on the host.
 ``decode_b1`` = the metric's second half: Qwen3-4B-architecture greedy decode
 tok/s at batch 1 (prompt 1024, 256 new tokens) against the weight-streaming
-roofline, with its own CPU baseline.
+roofline, with its own CPU baseline (Transformers' Qwen3ForCausalLM on the
+host, same weights and prompt). ``decode_b16`` = the same at batch 16;
+``layer_2048`` = one decoder layer at 2048 cached keys, batch 1, 4 and 16;
+``attention_ragged_b64`` = ragged decode attention at batch 64.
 """
 
 import argparse
@@ -71,34 +75,57 @@ def attn_bytes():
 
 
 def cpu_baseline(seconds):
-    """Time the CPU oracle (fp32 closed form) on 2 of the 16 sequences at full
-    context, repeated for about ``seconds``; report GB/s of the same algorithmic
-    bytes (K+V+q+out of the sample)."""
+    """The reference's CPU path for this attention call: torch SDPA in bf16, the
+    call Transformers' sdpa attention makes for a decode step (one query token,
+    enable_gqa), on the full workload (B=16 x 8192 keys, the same shapes and
+    seeded N(0,1) values as the GPU leg), repeated for about ``seconds``; GB/s of
+    the same algorithmic bytes."""
     import torch
-    from oracle import attention as A
+    import torch.nn.functional as F
     g = torch.Generator().manual_seed(0)
-    nb = 2
-    q = torch.randn(nb, NQ * D, generator=g).to(torch.bfloat16)
-    k = torch.randn(nb, NKV, CTX, D, generator=g).to(torch.bfloat16)
-    v = torch.randn(nb, NKV, CTX, D, generator=g).to(torch.bfloat16)
-    A.decode_attention(q, k, v, [CTX] * nb, dtype=torch.float32)  # warm
+    q = torch.randn(B, NQ, 1, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, NKV, CTX, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, NKV, CTX, D, generator=g).to(torch.bfloat16)
+    F.scaled_dot_product_attention(q, k, v, scale=D ** -0.5, enable_gqa=True)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
-        A.decode_attention(q, k, v, [CTX] * nb, dtype=torch.float32)
+        F.scaled_dot_product_attention(q, k, v, scale=D ** -0.5, enable_gqa=True)
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    nbytes = A.hbm_bytes(nb, NKV, [CTX] * nb, NQ)
     return {
-        "value": round(nbytes * n / el / 1e9, 3),
+        "value": round(attn_bytes() * n / el / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"oracle.attention.decode_attention fp32 on 2 of 16 sequences x 8192 keys "
-                  f"(32q/8kv, d128), {n} calls in {el:.1f} s; affinity "
-                  f"{len(os.sched_getaffinity(0))} cpus",
+        "kind": "reference",
+        "sample": f"torch scaled_dot_product_attention, bf16, enable_gqa (Transformers' sdpa "
+                  f"decode attention), the full B=16 x 8192-key workload, {n} calls in {el:.1f} s; "
+                  f"{torch.get_num_threads()} threads, affinity {len(os.sched_getaffinity(0))} cpus",
     }
+
+
+def hf_qwen3_cpu(cfg, w):
+    """Transformers' Qwen3ForCausalLM (sdpa attention) on the CPU in bf16 with the
+    given decode-layout weights (kernel_optim_amd.model.to_hf_state_dict): built
+    on the meta device and given the weights in place, so no random init runs."""
+    import torch
+    from transformers import Qwen3Config as HC, Qwen3ForCausalLM
+    from kernel_optim_amd.model import to_hf_state_dict
+    hc = HC(hidden_size=cfg.hidden, intermediate_size=cfg.inter, num_hidden_layers=cfg.layers,
+            num_attention_heads=cfg.nq, num_key_value_heads=cfg.nkv, head_dim=cfg.head_dim,
+            vocab_size=cfg.vocab, rms_norm_eps=cfg.eps, rope_theta=cfg.theta,
+            tie_word_embeddings=cfg.tied, max_position_embeddings=40960,
+            attn_implementation="sdpa")
+    with torch.device("meta"):
+        m = Qwen3ForCausalLM(hc)
+    m = m.to_empty(device="cpu").to(torch.bfloat16)
+    missing, unexpected = m.load_state_dict(to_hf_state_dict(cfg, w), strict=False, assign=True)
+    assert not unexpected and all(k == "lm_head.weight" for k in missing), (missing, unexpected)
+    if cfg.tied:
+        m.lm_head.weight = m.model.embed_tokens.weight
+    m.model.rotary_emb.__init__(hc)  # its inv_freq buffer was left on the meta device
+    return m.eval()
 
 
 def bench_decode(args, eng=None, B=1):
@@ -150,7 +177,10 @@ def bench_decode(args, eng=None, B=1):
     if eng.step_kind == "fused":
         res["gemv_cfg"] = {k: [list(g.cfg), round(g.us, 2)] for k, g in eng.gv.items()}
     if not args.no_cpu and B == 1:
-        res["cpu_baseline"] = cpu_decode_baseline(eng, args.cpu_seconds)
+        cb = cpu_decode_baseline(eng, prompt, args.cpu_seconds)
+        if "first_token" in cb:   # the prefill's greedy token, on both paths
+            cb["first_token_matches_gpu"] = cb["first_token"] == out[0]
+        res["cpu_baseline"] = cb
     return res
 
 
@@ -274,15 +304,53 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     return res
 
 
-def cpu_decode_baseline(eng, seconds):
-    """The oracle's eager Qwen3 forward on the host CPU with the same weights:
-    prefill a 16-token prompt, then time single-token decode steps for about
-    ``seconds`` (weight streaming dominates a decode step, so the short context
-    understates the CPU's per-token cost only slightly)."""
+def cpu_decode_baseline(eng, prompt, seconds):
+    """The reference's CPU path for the decode workload: Transformers'
+    Qwen3ForCausalLM (sdpa attention) in bf16 with the engine's weights, greedy
+    with a DynamicCache on the same 1024-token prompt; the prefill is timed on
+    its own, then one-token decode steps for about ``seconds`` (a bounded sample
+    of the 255 steps). Falls back to the oracle's eager forward (kind "port")
+    where Transformers is not importable."""
     import torch
     from kernel_optim_amd.model import weights_to
-    from oracle.qwen3 import Qwen3Oracle
     w = weights_to(eng.w, "cpu")
+    try:
+        from transformers import DynamicCache
+        m = hf_qwen3_cpu(eng.cfg, w)
+    except ImportError:
+        return cpu_decode_baseline_port(eng, w, seconds)
+    ids = torch.tensor(prompt, dtype=torch.int64)
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        out = m(input_ids=ids, past_key_values=DynamicCache(), use_cache=True)
+        prefill_s = time.perf_counter() - t0
+        tok = out.logits[:, -1].float().argmax(-1, keepdim=True)
+        first = int(tok[0, 0])
+        n, t0 = 0, time.perf_counter()
+        while True:
+            out = m(input_ids=tok, past_key_values=out.past_key_values, use_cache=True)
+            tok = out.logits[:, -1].float().argmax(-1, keepdim=True)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 255:
+                break
+    del m, w
+    return {"value": round(n / el, 4), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "prefill_s": round(prefill_s, 3), "first_token": first,
+            "sample": f"Transformers {__import__('transformers').__version__} Qwen3ForCausalLM "
+                      f"(sdpa), bf16, the same 36-layer weights, B=1, the same 1024-token "
+                      f"prompt with a DynamicCache: prefill {prefill_s:.1f} s, then {n} greedy "
+                      f"decode steps in {el:.1f} s; {torch.get_num_threads()} threads, affinity "
+                      f"{len(os.sched_getaffinity(0))} cpus"}
+
+
+def cpu_decode_baseline_port(eng, w, seconds):
+    """The oracle's eager Qwen3 forward on the host CPU with the same weights
+    (used only where Transformers is not importable): prefill a 16-token prompt,
+    then time single-token decode steps for about ``seconds``."""
+    import torch
+    from oracle.qwen3 import Qwen3Oracle
     n_max = 64
     orc = Qwen3Oracle(eng.cfg, w, B=1, cap=16 + n_max)
     prompt = torch.randint(0, eng.cfg.vocab, (1, 16), generator=torch.Generator().manual_seed(0))

@@ -138,15 +138,17 @@ def accept(draft_row, got_row):
 
 
 def _rope_tables(n, d, theta, device):
-    """cos/sin [n, d] bf16, Qwen3RotaryEmbedding's construction (fp32 on the CPU,
-    rounded to bf16), as the reference takes them from model.rotary_emb
-    (engine.py:164-171)."""
-    inv_freq = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.int64).to(torch.float32) / d))
-    pos = torch.arange(n, dtype=torch.int64).to(torch.float32)
-    freqs = pos[:, None] * inv_freq[None, :]
+    """cos/sin [n, d] bf16 for positions 0..n-1, computed as the reference takes
+    them from model.rotary_emb on the GPU (engine.py:164-171): Qwen3RotaryEmbedding's
+    inv_freq built in fp32 on the host, the frequencies as its fp32 product with
+    the positions, cos and sin in fp32 on the device, rounded to bf16."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+    inv = inv_freq[None, :, None].float().to(device)
+    pos = torch.arange(n, device=device)[None, None, :].float()
+    freqs = (inv @ pos).transpose(1, 2)
     emb = torch.cat((freqs, freqs), dim=-1)
-    return (emb.cos().to(torch.bfloat16).to(device).contiguous(),
-            emb.sin().to(torch.bfloat16).to(device).contiguous())
+    return (emb.cos()[0].to(torch.bfloat16).contiguous(),
+            emb.sin()[0].to(torch.bfloat16).contiguous())
 
 
 def _log(msg):

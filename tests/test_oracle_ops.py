@@ -55,6 +55,18 @@ def test_rope_tables_match_rotary_module(theta):
     assert torch.equal(c, cos[0]) and torch.equal(s, sin[0])
 
 
+@pytest.mark.parametrize("theta", [1.0e6, 5.0e6])
+def test_engine_rope_tables_match_rotary_module(theta):
+    """The engine's tables (computed with the module's recipe, here on the CPU)
+    equal Qwen3RotaryEmbedding's forward bit for bit."""
+    from kernel_optim_amd.engine import _rope_tables
+    rot = MQ.Qwen3RotaryEmbedding(cfg(theta))
+    n = 3000
+    cos, sin = rot(torch.empty(1, dtype=BF), torch.arange(n).unsqueeze(0))
+    c, s = _rope_tables(n, 128, theta, "cpu")
+    assert torch.equal(c, cos[0]) and torch.equal(s, sin[0])
+
+
 @pytest.mark.parametrize("T", [1, 3])
 def test_qk_norm_rope_matches_hf_attention_prologue(T):
     B, nq, nkv, d, cap = 2, 32, 8, 128, 64

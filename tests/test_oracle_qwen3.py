@@ -82,3 +82,22 @@ def test_weight_byte_counts_match_the_qwen3_4b_layout():
     cfg = Qwen3Config()
     assert cfg.layer_bytes() == 201_861_632
     assert cfg.weight_bytes_per_step() == 8_044_936_192
+
+
+def test_bench_transformers_builder_matches_a_plain_build():
+    """bench.py's CPU baseline builds Transformers' Qwen3ForCausalLM on the meta
+    device and hands it the weights in place (no random init of 4B parameters);
+    it must compute what a plain construction + load_state_dict computes, with
+    the rotary inv_freq buffer in fp32 as from_pretrained(torch_dtype=bf16)
+    leaves it (hf_model's blanket .to(bf16) rounds that buffer too)."""
+    import bench
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=3)
+    prompt = torch.randint(0, cfg.vocab, (2, 20), generator=torch.Generator().manual_seed(4))
+    plain = hf_model(cfg, w, "sdpa")
+    plain.model.rotary_emb.__init__(plain.config)
+    assert plain.model.rotary_emb.inv_freq.dtype == torch.float32
+    with torch.no_grad():
+        want = plain(input_ids=prompt).logits
+        got = bench.hf_qwen3_cpu(cfg, w)(input_ids=prompt).logits
+    assert torch.equal(got, want)
