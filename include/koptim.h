@@ -64,6 +64,24 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
                    float scale, float* o_part, float* ml, int* counters, void* out,
                    void* stream);
 
+/* ko_decode_attn in its two-launch form (partials, then the log-sum-exp
+ * combine) with no caller scratch and no allocation: the fp32 partials live in
+ * a fixed 16 MiB device array of the library (one per GPU, held until the
+ * process ends; its address is looked up on the first call on each device).
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Rejects with KO_ERANGE, before launching anything, a call whose
+ * partials exceed the array: B*T*nq*max_units*(head_dim + 2) floats (plus up
+ * to 63 of alignment) must fit in 4,194,304, e.g. B = 16 with 8192-key caches
+ * and 4096-key units, or B = 1 with up to 1000 units. Every call on a GPU uses
+ * that GPU's one array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be ordered by the caller. Other arguments as for
+ * ko_decode_attn. */
+int ko_decode_attn_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                           const int* kv_lens, int len_offset, int cap, long long cache_b_stride,
+                           long long cache_h_stride, int B, int T, int nkv, int head_dim, int unit,
+                           int max_units, int grid_waves, float scale, void* out, void* stream);
+
 /* DecodeAttention.__call__ for T = 2..8 query tokens per sequence (the verify
  * step, engine/engine.py:409-411 with fused.py:221-234), computed as B*T rows of
  * the one-token kernel: row b*T + t attends keys 0 .. pos[b] + t of sequence b

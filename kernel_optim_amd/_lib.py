@@ -56,6 +56,9 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                                  _c_void_p, _int, _c_void_p, _c_void_p],
     "ko_decode_attn_qkv_oproj_sync_ints": [],
+    "ko_decode_attn_noalloc": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll,
+                               _int, _int, _int, _int, _int, _int, _int, _f, _c_void_p,
+                               _c_void_p],
     "ko_decode_attn_token_rows": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll,
                                   _int, _int, _int, _int, _int, _int, _int, _f, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p],

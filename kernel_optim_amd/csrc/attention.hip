@@ -36,7 +36,17 @@
 //           next launch.
 #include "attn_core.h"
 
+#include <mutex>
+
 using namespace ko;
+
+// Scratch of ko_decode_attn_noalloc: the fp32 partials (o_part, then ml) of the
+// two-launch form, in a fixed device array instead of caller or library
+// allocations. Each GPU the library runs on holds its own copy, for the life of
+// the process; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (noalloc_scratch below).
+constexpr long long KO_NOALLOC_SCRATCH_FLOATS = (16LL << 20) / 4;  // 16 MiB
+static __device__ __align__(256) float scratch[KO_NOALLOC_SCRATCH_FLOATS];
 
 namespace {
 
@@ -692,6 +702,54 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
 }
 
 long long ko_decode_attn_qkv_oproj_sync_ints(void) { return OPROJ_SYNC_INTS; }
+
+}  // extern "C"
+
+namespace {
+
+constexpr int KO_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[KO_MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept; 0 on success.
+int noalloc_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= KO_MAX_DEVICES) return KO_ENOTSUP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return KO_EINVAL;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return KO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ko_decode_attn_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                           const int* kv_lens, int len_offset, int cap, long long cache_b_stride,
+                           long long cache_h_stride, int B, int T, int nkv, int head_dim, int unit,
+                           int max_units, int grid_waves, float scale, void* out, void* stream) {
+  if (B < 1 || T < 1 || nkv < 1 || max_units < 1 || head_dim != D) return KO_EINVAL;
+  const long long rows = (long long)B * T * nkv * G;
+  const long long n_part = rows * max_units * D;
+  const long long off_ml = (n_part + 63) / 64 * 64;  // ml starts 256-byte aligned
+  if (off_ml + rows * max_units * 2 > KO_NOALLOC_SCRATCH_FLOATS) return KO_ERANGE;
+  float* base = nullptr;
+  int st = noalloc_scratch(&base);
+  if (st) return st;
+  return ko_decode_attn(q, k_cache, v_cache, kv_lens, len_offset, cap, cache_b_stride,
+                        cache_h_stride, B, T, nkv, head_dim, unit, max_units, grid_waves, scale,
+                        base, base + off_ml, nullptr, out, stream);
+}
 
 int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, const void* cos,
                              const void* sin, int max_pos, const int* pos, void* k_cache,
