@@ -31,12 +31,11 @@ extern "C" {
  * unit     keys per work unit (multiple of 16); max_units*unit >= cap. Each unit
  *          leaves one fp32 partial slot per query row.
  * grid_waves  number of wavefronts launched (they stride over the units). With
- *          T == 1 a unit is split over the wavefronts of one workgroup: 8 when
- *          unit >= 1024 and unit % 128 == 0, else 4 when unit % 64 == 0, else 2
- *          when unit % 32 == 0, else 1, so grid_waves should be a multiple of
- *          that count.
+ *          T == 1 a unit is split over the wavefronts of one workgroup: 4 when
+ *          unit % 64 == 0, else 2 when unit % 32 == 0, else 1, so grid_waves
+ *          should be a multiple of that count.
  * o_part   [B*T*nq*max_units*head_dim] fp32 scratch, ml [B*T*nq*max_units*2] fp32.
- * T in 1..4, head_dim 128. */
+ * T in 1..8 (T > 4 runs as two launches of 2-4 query tokens), head_dim 128. */
 int ko_decode_attn_partial(const void* q, const void* k_cache, const void* v_cache,
                            const int* kv_lens, int len_offset, int cap,
                            long long cache_b_stride, long long cache_h_stride, int B, int T,
@@ -53,11 +52,10 @@ int ko_decode_attn_combine(const float* o_part, const float* ml, const int* kv_l
 /* The whole of DecodeAttention.__call__ (fused.py:221-234). With counters == NULL:
  * ko_decode_attn_partial followed by ko_decode_attn_combine, the reference's
  * two launches. With counters ([B*nkv] int32, zero before the first call;
- * every call leaves them zero) it is one launch: the last work unit of each
- * (sequence, KV head) merges that pair's partials. For T == 1 the partials and
- * the arrival count travel through device-coherent (agent-scope) stores, loads
- * and atomics; for T > 1 each unit publishes its partials with a device-scope
- * fence. */
+ * every call leaves them zero) it is one launch per group of up to 4 query
+ * tokens: the last work unit of each (sequence, KV head) merges that pair's
+ * partials. The partials and the arrival count travel through device-coherent
+ * (agent-scope) stores, loads and atomics; no fence or L2 write-back. */
 int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens,
                    int len_offset, int cap, long long cache_b_stride, long long cache_h_stride,
                    int B, int T, int nkv, int head_dim, int unit, int max_units, int grid_waves,
@@ -117,8 +115,8 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
                        void* stream);
 
 /* ko_decode_attn_qkv (with counters) and the o projection with its residual add
- * in ONE launch, for B <= 2 and unit % 64 == 0, unit < 1024 (4 wavefronts per
- * unit): out [B, nq*head_dim] receives the merged attention output as before,
+ * in ONE launch, for B <= 2 and unit % 64 == 0 (4 wavefronts per unit) and an
+ * o-projection input width nq*head_dim <= 4096: out [B, nq*head_dim] receives the merged attention output as before,
  * and h [B, H] <- bf16(h + bf16(out @ w_o^T)) (w_o [H, nq*head_dim] bf16), the
  * RESID GEMV of engine/engine.py:330-331 (kernels/gemv.py EPI_RESID). Extra
  * workgroups own 8 columns of the projection each; they load their weights while

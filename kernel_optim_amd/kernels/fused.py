@@ -66,10 +66,9 @@ class DecodeAttention:
 
     A second launch merges the partials, as the reference does; with
     ``fused_combine`` the last unit of each (sequence, KV head) merges them in
-    the same launch instead, through an arrival counter. For one query token
-    the partials travel through device-coherent stores and loads (no L2
-    write-back); for T > 1 a device-scope fence per unit publishes them, which
-    costs an L2 write-back on MI355X.
+    the same launch instead, through an arrival counter. The partials and the
+    counter travel through device-coherent stores, loads and atomics (no fence,
+    no L2 write-back).
     """
 
     MAX_T = 8
