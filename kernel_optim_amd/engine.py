@@ -300,6 +300,7 @@ class Engine:
         # ids of step j land in row j: the prefill's by a copy, the decode steps'
         # straight from the LM head's tail (ring_ctr: the next row it writes)
         self.pin_ids = torch.empty(N + 1, B, dtype=torch.int64, pin_memory=True)
+        self._ring_np = self.pin_ids.numpy()
         self.ring_ctr = torch.zeros(B, dtype=torch.int32, device=dev)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
@@ -589,17 +590,20 @@ class Engine:
         if self.K:
             yield from self._generate_spec(input_ids, N, stream)
             return
-        # The fused step writes its ids into row ring_ctr of ids_h itself; the
-        # hipBLASLt step's ids are copied after each replay.
+        # The fused step writes its ids into row ring_ctr of ids_h itself, so the
+        # host waits for row j to fill (rows start at -1) instead of recording
+        # an event per step; the hipBLASLt step's ids are copied after each
+        # replay and waited for with an event.
         ring = self.step_kind == "fused"
         if ring:
+            self._ring_np[1:] = -1
             self.ring_ctr.fill_(1)
         # Keep one replay in flight: queue step j before waiting for step j-1.
         if N > 1:
             self.g1.replay()
             if not ring:
                 ids_h[1].copy_(self.ids, non_blocking=True)
-            ev[1].record(stream)
+                ev[1].record(stream)
         ev[0].synchronize()
         yield ids_h[0].tolist()
         for j in range(1, N):
@@ -607,11 +611,29 @@ class Engine:
                 self.g1.replay()
                 if not ring:
                     ids_h[j + 1].copy_(self.ids, non_blocking=True)
-                ev[j + 1].record(stream)
-            ev[j].synchronize()
+                    ev[j + 1].record(stream)
+            if ring:
+                self._wait_row(j)
+            else:
+                ev[j].synchronize()
             if j == N - 1:
                 self.attn.check_sync()   # raises if a fused o-projection wait gave up
             yield ids_h[j].tolist()
+
+    def _wait_row(self, j, timeout_s=60.0):
+        """Wait until the decode step that writes row j of the pinned id ring has
+        stored every sequence's id (the LM head's tail stores them from the GPU;
+        the rows start at -1)."""
+        row = self._ring_np[j]
+        if (row >= 0).all():
+            return
+        t_end = time.monotonic() + timeout_s
+        while not (row >= 0).all():
+            if time.monotonic() > t_end:
+                torch.cuda.synchronize()
+                if (row >= 0).all():
+                    return
+                raise RuntimeError(f"decode step {j} stored no ids in the host ring")
 
     def _generate_spec(self, input_ids, N, stream):
         """generate() with prompt-lookup speculation (engine.py:435-508): verify
