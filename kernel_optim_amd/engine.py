@@ -404,19 +404,24 @@ class Engine:
         rope_rows(self.pos, self._cos, self._sin, self.rope)
 
     def _time_graph(self, g, reps=10):
-        """Mean replay time (ms) of a captured step from positions where every
-        cache write stays inside the capacity."""
-        start = max(0, min(self.S, self.cap - (reps + 2) - (self.K + 1)))
+        """GPU time (ms) of one replay of a captured step: the median of ``reps``
+        replays, each between its own pair of events, after one untimed replay.
+        The replays start at the prompt's end, or earlier where the cache slots
+        they write (one per replay for the one-token step, K + 1 for the verify
+        step) would pass the capacity."""
+        span = max(reps + 1, self.K + 1) + 1
         torch.cuda.synchronize()
-        self._set_pos(start)
+        self._set_pos(max(0, min(self.S, self.cap - span)))
         g.replay()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
+        marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(reps)]
+        for a, b in marks:
+            a.record()
             g.replay()
-        b.record()
+            b.record()
         torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
+        times = sorted(a.elapsed_time(b) for a, b in marks)
+        return times[len(times) // 2]
 
     def _tiled(self, name, weights):
         """MFMA-layout copies of one projection's weights (kernels.gemv.tile_weights),
@@ -510,23 +515,27 @@ class Engine:
             torch.mm(self.nT, self.w["lm_head"].t(), out=self.logitsT)
             argmax_rows(self.logitsT, self.vout.view(-1))
 
-    def _capture(self, fn):
-        # Warm up on a side stream, then capture. Warm-up steps write cache slot 0,
-        # which the prefill of every generate() call overwrites.
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for _ in range(2):
-                self.pos.zero_()
+    def _capture(self, fn, warmups=2):
+        """A hipGraph of one call of ``fn`` (torch's documented capture recipe):
+        ``fn`` first runs ``warmups`` times eagerly on a side stream, so every
+        code object is loaded and every buffer it touches exists, then once
+        under capture. The eager calls write cache slot 0 (positions 0), which
+        every prefill overwrites."""
+        main = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for _ in range(warmups):
+                self._set_pos(0)
                 fn()
-        torch.cuda.current_stream().wait_stream(s)
+        main.wait_stream(side)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
+        graph = torch.cuda.CUDAGraph()
         self._set_pos(0)
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(graph):
             fn()
         torch.cuda.synchronize()
-        return g
+        return graph
 
     # ---------------------------------------------------------------- forward
     def _prefill(self, prompt):
