@@ -13,7 +13,7 @@ Qwen3-4B-architecture model the benchmarks run.
 import glob
 import json
 import os
-from dataclasses import asdict, dataclass
+from dataclasses import dataclass
 
 import torch
 
@@ -170,6 +170,3 @@ def save_checkpoint(path, cfg, weights):
         del sd["lm_head.weight"]
     save_file(sd, os.path.join(path, "model.safetensors"))
 
-
-def config_dict(cfg):
-    return asdict(cfg)
