@@ -108,13 +108,16 @@ def test_two_generate_calls_do_not_share_state(dev):
     assert a == a2 and len(b) == 6 and all(len(x) == 2 for x in b)
 
 
-@pytest.mark.parametrize("B,S", [(1, 1024), (16, 1024), (4, 2048)])
-def test_engine_full_size_decode(dev, B, S):
+@pytest.mark.parametrize("B,S,n", [(1, 1024, 256), (16, 1024, 256), (4, 2048, 256),
+                                   (1, 8192, 64)])
+def test_engine_full_size_decode(dev, B, S, n):
     """The decode workload at full size: Qwen3-4B architecture (36 layers, random
-    N(0, 0.02) bf16 weights), prompts of S seeded random ids, 256 greedy tokens;
-    B = 1 and 16 at S = 1024 (the benchmark's decode workloads) and B = 4 at
+    N(0, 0.02) bf16 weights), prompts of S seeded random ids, n greedy tokens;
+    B = 1 and 16 at S = 1024 (the benchmark's decode workloads), B = 4 at
     S = 2048 (the reference contract's public batch-4 workload,
-    QWEN_ENGINE_CONTRACT.md:79). The reference eager path replays the emitted
+    QWEN_ENGINE_CONTRACT.md:79) and B = 1 at S = 8192 (long context: RoPE and
+    the KV append past position 8192, 32-unit attention splits per KV head).
+    The reference eager path replays the emitted
     tokens decode-shaped (one forward per token, as generate() with a KV cache
     runs): every token must be within the tie margin and the 2x-error rule, the
     logits within FULL_LOGIT_ATOL and the greedy agreement at least
@@ -123,7 +126,6 @@ def test_engine_full_size_decode(dev, B, S):
     under a change of GEMM shapes."""
     cfg = Qwen3Config()
     w = random_weights(cfg, seed=0, device=dev)
-    n = 256
     prompt = torch.randint(0, cfg.vocab, (B, S), generator=torch.Generator().manual_seed(B))
     eng = _engine(cfg, w)
     toks, logits = eng.trace(prompt.tolist(), n)
@@ -137,7 +139,7 @@ def test_engine_full_size_decode(dev, B, S):
     ref_noise = float((replay.float() - prefill_shaped.float()).abs().max())
     agree, err = check_against_replay(toks, logits, replay)
     agree_p = float((prefill_shaped.float().argmax(-1) == toks).float().mean())
-    print(f"full size B={B} S={S}: greedy agreement {agree:.4f} (prefill-shaped replay "
+    print(f"full size B={B} S={S} n={n}: greedy agreement {agree:.4f} (prefill-shaped replay "
           f"{agree_p:.4f}), max |dlogit| {err:.4f}; reference decode- vs prefill-shaped "
           f"{ref_noise:.4f}")
     assert err <= FULL_LOGIT_ATOL
