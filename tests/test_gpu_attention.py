@@ -166,6 +166,28 @@ def test_config3_ragged_padded_tail_unread(dev):
 
 
 @pytest.mark.parametrize("fused_combine", [False, True])
+def test_long_context_65536(dev, fused_combine):
+    """Two sequences of 65536 and 40001 keys in a 65536-slot cache (the sizing rule
+    then takes 2048-key units, 32 per KV head) against fp32 attention; the unused
+    tail of the shorter sequence is NaN, so reading it would poison the output."""
+    fused = _fused()
+    B, cap = 2, 65536
+    lens = torch.tensor([65536, 40001], dtype=torch.int32)
+    q, k, v = _inputs(B, 1, cap, dev, seeds=(20, 21, 22))
+    k[1, :, 40001:] = float("nan")
+    v[1, :, 40001:] = float("nan")
+    out = torch.empty_like(q)
+    att = fused.DecodeAttention(B, 1, cap, 32, 8, 128, dev, fused_combine=fused_combine)
+    att.with_lengths(q, k, v, lens.to(dev), out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    ref = _gpu_ref_fp32(q, k, v, lens.tolist())
+    torch.testing.assert_close(out.float(), ref, **TOL)
+    if fused_combine:
+        assert torch.all(att.counters == 0)
+
+
+@pytest.mark.parametrize("fused_combine", [False, True])
 def test_more_than_64_sequences(dev, fused_combine):
     """B = 130: the pair lookup past one wavefront's 64 lengths (three chunks of
     lengths, the last partly filled), ragged lengths in 1..640, NaN beyond each."""
