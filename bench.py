@@ -230,7 +230,8 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     cannot serve a replay; the replays are captured in one graph and timed with
     events."""
     import torch
-    from kernel_optim_amd.engine import _rope_tables, build_decode_gemvs, decode_layer
+    from kernel_optim_amd.engine import (_rope_tables, attn_units_per_seq, build_decode_gemvs,
+                                         decode_layer)
     from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
     from kernel_optim_amd.kernels.gemv import tile_weights
     from kernel_optim_amd.model import Qwen3Config, random_weights
@@ -261,7 +262,8 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         act = torch.empty(B, cfg.inter, device=dev, dtype=torch.bfloat16)
         # the engine's decode step: fused combine, the step's RoPE rows once, and the
         # o projection in the attention's launch where it fits (B <= 2)
-        att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True)
+        att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True,
+                              units_per_seq=attn_units_per_seq(B, cfg.nkv))
         att.oproj_delay_ns = 500
         rope = torch.empty(B, 2, cfg.head_dim, device=dev, dtype=torch.bfloat16)
         fuse_o = att.oproj_fusable()

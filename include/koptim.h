@@ -105,14 +105,19 @@ int ko_decode_attn_token_rows(const void* q, const void* k_cache, const void* v_
  * rope (optional, [B][2][head_dim] bf16, 16-byte aligned): the cos and sin rows
  * at pos[b] as ko_rope_rows writes them; the kernel then reads them instead of
  * the table rows behind the position, and for B == 1 (with a unit per
- * workgroup) issues its first loads before it reads the position. */
+ * workgroup) issues its first loads before it reads the position.
+ * units_per_seq = 0: units of `unit` keys. units_per_seq = U > 0 (counters
+ * given, B <= 64, unit % 64 == 0): each sequence's pos[b] + 1 keys are cut
+ * into at most U units of equal size, rounded up to a multiple of 64 and at
+ * least `unit` keys, from its length at this step (max_units * unit >= cap
+ * still sizes the partials). */
 int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const void* cos,
                        const void* sin, int max_pos, const int* pos, void* k_cache,
                        void* v_cache, int cap, long long cache_b_stride,
                        long long cache_h_stride, int B, int nkv, int head_dim, int unit,
                        int max_units, int grid_waves, float eps, float scale, float* o_part,
                        float* ml, int* counters, void* out, const void* rope,
-                       void* stream);
+                       int units_per_seq, void* stream);
 
 /* ko_decode_attn_qkv (with counters) and the o projection with its residual add
  * in ONE launch, for B <= 2 and unit % 64 == 0 (4 wavefronts per unit) and an

@@ -29,7 +29,7 @@ SIGNATURES = {
     "ko_decode_attn_qkv": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int,
                            _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll, _int, _int, _int,
                            _int, _int, _int, _f, _f, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                           _c_void_p, _c_void_p],
+                           _c_void_p, _int, _c_void_p],
     "ko_rope_rows": [_c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _c_void_p, _c_void_p],
     "ko_add_rms_norm": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _f, _c_void_p],
     "ko_qk_norm_rope": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

@@ -672,12 +672,17 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
                        void* v_cache, int cap, long long cache_b_stride,
                        long long cache_h_stride, int B, int nkv, int head_dim, int unit,
                        int max_units, int grid_waves, float eps, float scale, float* o_part,
-                       float* ml, int* counters, void* out, const void* rope, void* stream) {
+                       float* ml, int* counters, void* out, const void* rope, int units_per_seq,
+                       void* stream) {
   int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
                         head_dim, unit, max_units, o_part, ml);
   if (st) return st;
   if (!qkv || !q_w || !k_w || !cos || !sin || !out || max_pos < 1 || grid_waves < 1)
     return KO_EINVAL;
+  if (units_per_seq < 0) return KO_EINVAL;
+  // per-sequence units: one wavefront split (4 per unit), the fused merge, and
+  // the small-batch unit enumeration
+  if (units_per_seq > 0 && (!counters || B > 64 || unit % 64)) return KO_ENOTSUP;
   if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
       !aligned16(sin) || !aligned16(out) || (rope && !aligned16(rope)))
     return KO_EINVAL;
@@ -693,6 +698,7 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
   a.counters = counters;
   a.out = static_cast<uint16_t*>(out);
   a.rope = static_cast<const uint16_t*>(rope);
+  a.usplit = units_per_seq;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (counters) return launch1<true, true>(a, grid_waves, s);
   st = launch1<true, false>(a, grid_waves, s);

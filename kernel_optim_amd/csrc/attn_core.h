@@ -43,6 +43,10 @@ struct AttnArgs {
   int len_off, cap;
   long long cb, ch;
   int B, nkv, unit, max_units;
+  // One-token kernel, B <= 64, fused merge: cut each sequence's keys into at
+  // most usplit units of equal size (a multiple of 64, at least `unit`) from
+  // its current length, instead of fixed units of `unit` keys (0: fixed).
+  int usplit;
   // Query tokens per sequence in the q / out / partial row layout (T of the
   // call), and the first token this launch serves: calls of more than 4
   // tokens run in launches of up to 4 (attn_kernel's tile holds 4 tokens x 4
@@ -65,6 +69,13 @@ struct AttnArgs {
 
 __device__ __forceinline__ int nunits(int len, int unit) {
   return len > 0 ? (len + unit - 1) / unit : 0;
+}
+// Keys per unit of a sequence of len keys: `unit`, or with usplit > 0 the
+// length cut into usplit parts, rounded up to a multiple of 64, at least `unit`.
+__device__ __forceinline__ int unit_for(int len, int unit, int usplit) {
+  if (usplit <= 0 || len <= 0) return unit;
+  const int u = ((len + usplit - 1) / usplit + 63) & ~63;
+  return u > unit ? u : unit;
 }
 __device__ __forceinline__ int seq_len(const int* lens, int b, int off, int cap, int rep = 1) {
   int l;
@@ -274,7 +285,8 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
   uint4 ka[4], va[4];
   uint32_t xh[NH], qwv = 0, cwv = 0, swv = 0, xk = 0, kwv = 0, vv = 0;
   uint4 vnew = make_uint4(0, 0, 0, 0);
-  const bool spec = QKV && a.B == 1 && a.rope != nullptr && nwg >= nkv * max_units;
+  const bool spec = QKV && a.B == 1 && a.rope != nullptr && a.usplit == 0 &&
+                    nwg >= nkv * max_units;
   if (spec && wg < nkv * max_units) {
     const int c = wg / nkv, kvh = wg - c * nkv;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(a.qkv);
@@ -311,11 +323,14 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     // vector loads above
     const int len = *(const __attribute__((address_space(4))) int*)a.lens + a.len_off;
     len1 = len < a.cap ? len : a.cap;
-    my_n = lane == 0 ? nunits(len1, unit) : 0;
+    my_n = lane == 0 ? nunits(len1, unit_for(len1, unit, a.usplit)) : 0;
     my_incl = readlane(my_n, 0);
     total = my_incl * nkv;
   } else if (small_b) {
-    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap, a.rep), unit) : 0;
+    if (lane < a.B) {
+      const int l = seq_len(a.lens, lane, a.len_off, a.cap, a.rep);
+      my_n = nunits(l, unit_for(l, unit, a.usplit));
+    }
     my_incl = wave_incl_scan(my_n);
     total = readlane(my_incl, 63) * nkv;
   } else {
@@ -344,9 +359,11 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       if (b < 0) break;  // unreachable while lens[] is unchanged during the launch
       kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap, a.rep));
     }
-    const int ku1 = min((c + 1) * unit, kv_len);
-    const int k0 = c * unit + wave * sub;
-    const int k1 = min(k0 + sub, ku1);
+    const int unit_b = unit_for(kv_len, unit, a.usplit);  // uniform: one sequence per unit
+    const int sub_b = a.usplit > 0 ? unit_b / WM : sub;
+    const int ku1 = min((c + 1) * unit_b, kv_len);
+    const int k0 = c * unit_b + wave * sub_b;
+    const int k1 = min(k0 + sub_b, ku1);
     const bool active = k0 < k1;  // the last unit of a sequence may leave waves idle
     const int pnew = kv_len - 1;
     const bool new_unit = QKV && pnew < ku1;  // this unit holds the new key position
@@ -633,7 +650,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       if (threadIdx.x == 0)
         lds_prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __syncthreads();
-      const int n = nunits(kv_len, unit);
+      const int n = nunits(kv_len, unit_b);
       if (lds_prev == n - 1) {
         for (int j = wave; j < G; j += WM)
           combine_row<32, true, Hooks::kNotify>(a.o_part, a.ml, (long long)b * nq + kvh * G + j,

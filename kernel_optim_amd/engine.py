@@ -57,6 +57,9 @@ FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
 OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "500"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
+# units per sequence of the one-token attention at B >= 3 (-1: one round of the
+# 256 CUs, 256 // (B * KV heads); 0: fixed units of ATTN_UNIT or the sizing rule)
+ATTN_SPLIT = int(os.environ.get("ENGINE_ATTN_SPLIT", "-1"))
 # decode-step graph: "auto" captures the fused-GEMV step and the hipBLASLt step for
 # batches up to FUSED_MAX_B and keeps the faster (engine.py:197-208); "fused" or
 # "hipblaslt" takes one
@@ -154,6 +157,17 @@ def _rope_tables(n, d, theta, device):
 def _log(msg):
     if LOG:
         print(f"[engine] {msg}", file=sys.stderr, flush=True)
+
+
+def attn_units_per_seq(B, nkv):
+    """Units per sequence of the one-token decode attention at batch B: at 3..64
+    sequences each sequence's keys are cut at every step into at most
+    256 // (B * nkv) equal units (one round of workgroups over the 256 CUs at
+    equal lengths); at B <= 2 (the attention + o projection launch) fixed units.
+    ENGINE_ATTN_SPLIT >= 0 overrides (0: fixed units)."""
+    if ATTN_SPLIT >= 0:
+        return ATTN_SPLIT
+    return max(1, 256 // (B * nkv)) if 3 <= B <= 64 else 0
 
 
 def build_decode_gemvs(cfg, M, raw, deadline, tiled_fn=None, tune=True, log=""):
@@ -304,7 +318,8 @@ class Engine:
         self.ring_ctr = torch.zeros(B, dtype=torch.int32, device=dev)
         self.events = [torch.cuda.Event() for _ in range(N + 1)]
         self.attn = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev,
-                                    unit=ATTN_UNIT or None, fused_combine=True)
+                                    unit=ATTN_UNIT or None, fused_combine=True,
+                                    units_per_seq=attn_units_per_seq(B, cfg.nkv))
         self.attn.oproj_delay_ns = OPROJ_DELAY_NS
         L = self.w["layers"]
         raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],

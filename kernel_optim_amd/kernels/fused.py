@@ -74,7 +74,7 @@ class DecodeAttention:
     MAX_T = 8
 
     def __init__(self, B, T, cap, nq, nkv, d, device, target_ctas=2048, unit=None,
-                 fused_combine=False, token_rows=False):
+                 fused_combine=False, token_rows=False, units_per_seq=0):
         _need(d == 128, "head_dim must be 128")
         _need(nq == 4 * nkv, "the kernel serves GQA groups of 4 query heads per KV head")
         _need(1 <= T <= self.MAX_T, f"T must be in 1..{self.MAX_T}")
@@ -86,6 +86,17 @@ class DecodeAttention:
         self.token_rows = bool(token_rows)
         wg_split = T == 1 or self.token_rows
         rows_k = B * T if self.token_rows else B  # rows the one-token kernel sizes for
+        # units_per_seq = U > 0: decode_qkv cuts each sequence's keys into at most U
+        # equal units (multiples of 64 keys, at least `unit`) from its length at
+        # each step, so a batch of equal lengths fills one round of the grid
+        # whatever the position (ko_decode_attn_qkv)
+        self.units_per_seq = int(units_per_seq)
+        if self.units_per_seq:
+            _need(self.units_per_seq > 0 and T == 1 and not self.token_rows and fused_combine
+                  and B <= 64, "units_per_seq serves one token per sequence, B <= 64, with "
+                  "the fused combine")
+            unit = 64 if unit is None else unit
+            _need(unit % 64 == 0, "units_per_seq needs a unit (the smallest unit) % 64 == 0")
         if unit is None:
             share = _cdiv(_cdiv(rows_k * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
             # one-token units stop at 2048 keys: past that, ragged lengths leave
@@ -105,7 +116,8 @@ class DecodeAttention:
         else:
             wpu = 4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1
         self.waves_per_unit = wpu
-        self.grid_waves = max(1, min(rows_k * nkv * self.max_units * wpu, target_ctas))
+        units = min(self.max_units, self.units_per_seq) if self.units_per_seq else self.max_units
+        self.grid_waves = max(1, min(rows_k * nkv * units * wpu, target_ctas))
         rows = B * T * nq
         self.o_part = torch.empty(rows * self.max_units * d, dtype=torch.float32, device=device)
         self.ml = torch.empty(rows * self.max_units * 2, dtype=torch.float32, device=device)
@@ -245,7 +257,7 @@ class DecodeAttention:
                   _lib.ptr(v_cache), self.cap, k_cache.stride(0), k_cache.stride(1), B, nkv, d,
                   self.unit, self.max_units, self.grid_waves, eps, self.scale,
                   _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters),
-                  _lib.ptr(out), _lib.ptr(rope), _lib.stream_ptr())
+                  _lib.ptr(out), _lib.ptr(rope), self.units_per_seq, _lib.stream_ptr())
 
 
 def rope_rows(pos, cos, sin, out):

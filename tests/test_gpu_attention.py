@@ -319,6 +319,61 @@ def test_decode_qkv_matches_norm_rope_append_then_attention(dev, B, cap, unit, f
     assert torch.equal(v.cpu(), vref)
 
 
+@pytest.mark.parametrize("B,cap,split", [(3, 1300, 10), (16, 1296, 2), (16, 700, 5),
+                                         (64, 600, 1), (2, 2100, 16)])
+def test_decode_qkv_units_per_seq(dev, B, cap, split):
+    """decode_qkv with each sequence's keys cut into at most `split` equal units from
+    its length at the step (units_per_seq): the oracle's qk_norm_rope then
+    attention over keys 0..pos, with ragged positions (the last slot, slot 0, 63,
+    64, random), over three graph-replayed steps whose positions advance; the
+    arrival counters re-arm every step."""
+    from oracle import ops as O
+    from tests.bf16util import assert_bf16_close
+    fused_mod = _fused()
+    nq, nkv, d = 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(90 + B + split)
+    qkv = torch.randn(B, (nq + 2 * nkv) * d, device=dev, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(d, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in O.rope_tables(cap, d, 1.0e6))
+    k = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, nkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
+    steps = 3
+    pos = torch.randint(0, cap - steps, (B,), device=dev, generator=g).to(torch.int32)
+    for i, p0 in enumerate((cap - steps, 0, 62, 63)[:B]):
+        pos[i] = p0
+    att = fused_mod.DecodeAttention(B, 1, cap, nq, nkv, d, dev, fused_combine=True,
+                                    units_per_seq=split)
+    out = torch.empty(B, nq * d, device=dev, dtype=torch.bfloat16)
+    kref, vref = k.cpu(), v.cpu()
+    pos_h = pos.cpu().clone()
+
+    def step():
+        att.decode_qkv(qkv, qw, kw, cos, sin, pos, k, v, out, 1e-6)
+        pos.add_(1)
+    s_ = torch.cuda.Stream()
+    s_.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_):
+        step()
+    torch.cuda.current_stream().wait_stream(s_)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for j in range(steps):
+        if j:
+            graph.replay()
+        torch.cuda.synchronize()
+        p = pos_h + j
+        qref = O.qk_norm_rope(qkv.cpu(), qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), p, kref, vref,
+                              1, 1e-6, nq, nkv, d)
+        want = A.decode_attention(qref, kref, vref, [int(x) + 1 for x in p])
+        torch.testing.assert_close(out.cpu().double(), want, **TOL)
+        assert torch.all(att.counters == 0)
+    assert_bf16_close(k.cpu(), kref, max_frac=1e-3)
+    assert torch.equal(v.cpu(), vref)
+
+
 def test_rope_rows_are_the_table_rows(dev):
     """rope_rows copies cos[p], sin[p] for each sequence's position, with p clamped
     to the table."""
