@@ -220,7 +220,9 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           wavefronts per workgroup; M <= 4 per launch slice.
  * layout 2: MFMA 16-column tiles, M <= 16 per launch slice (rows padded with
  *           zeros), K in {2560, 4096, 9728} (SWIGLU: 2560, 4096); a persistent
- *           grid of 256 * `rows` (1, 2 or 4) workgroups. w must be in the tiled
+ *           grid of at most 256 * `rows` (1, 2 or 4) workgroups, the fewest
+ *           that keep the most tiles per workgroup at its minimum (384 tiles:
+ *           192 workgroups of 2). w must be in the tiled
  *           layout written by ko_gemv_tile (for SWIGLU: the gate rows tiled,
  *           then the up rows tiled, each padded to a multiple of 16 rows).
  * layout 3: layout 2's tiles and weight copy with the K range of a tile cut

@@ -10,23 +10,32 @@
 namespace ko {
 
 constexpr int LDS_X_BYTES = 40960;  // layout 1: normalised x staged for the workgroup (M*K*2)
-constexpr int MFMA_CUS = 256;       // MI355X compute units: layout-2 persistent grid = 256 x rows
+constexpr int MFMA_CUS = 256;       // MI355X compute units: layout-2 grid of at most 256 x rows
 constexpr int KS_MAX = 32;          // layout 3: slices per tile
 
 // layout 0: `rows` (4, 8; 16 for M <= 2) columns per 256-thread workgroup
 int launch_layout0(const GemvArgs& a, int epi, bool norm, int rows, hipStream_t s);
 // layout 1: `rw` columns per wavefront, `wpb` wavefronts per workgroup
 int launch_layout1(const GemvArgs& a, int epi, bool norm, int rw, int wpb, hipStream_t s);
-// layout 2: MFMA tiles, a persistent grid of MFMA_CUS * per_cu workgroups
+// layout 2: MFMA tiles, a persistent grid of at most MFMA_CUS * per_cu workgroups
 int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s);
 // layout 3: MFMA tiles with the K range cut into `slices`
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s);
 
+// Workgroups of the layout-2 grid: at most MFMA_CUS * per_cu, and of those the
+// fewest that keep the most tiles per workgroup at its minimum, so every
+// workgroup runs the same number of tiles (but the last ones, one fewer). A
+// part-filled last round leaves the busy workgroups as long as the full ones
+// and only spreads the weights over more CUs: 16 rows, 384 tiles on 192
+// workgroups 10.14 against 10.52 us on 256; 608 tiles on 203 workgroups 19.85
+// against 20.70 us.
 inline int mfma_grid(int N, int per_cu) {
   const int ntiles = (N + 15) / 16;
   const int g = MFMA_CUS * per_cu;
-  return ntiles < g ? ntiles : g;
+  if (ntiles <= g) return ntiles;
+  const int rounds = (ntiles + g - 1) / g;
+  return (ntiles + rounds - 1) / rounds;
 }
 
 // K = 32 * S * WPG: S steps of 32 per wavefront, WPG wavefronts splitting K.

@@ -92,7 +92,8 @@ class Gemv:
         Layout 1 (a wavefront per row group) is the batch-1..4 path; layout 0
         serves every batch up to 16 rows per launch with VALU dot products;
         layout 2 puts 2..16 rows on MFMA (``(2, per_cu, 0)``: a persistent grid
-        of 256 x per_cu workgroups) and layout 3 splits its tiles' K range."""
+        of at most 256 x per_cu workgroups, the fewest that keep the most tiles
+        per workgroup at its minimum) and layout 3 splits its tiles' K range."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
         mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
