@@ -234,6 +234,14 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           scratch (part_len >= ko_gemv_argmax_scratch(N, 3, rows, 0)): zero
  *           before the first call, left zero by every call (the tiles' arrival
  *           counters); calls that share it must not overlap.
+ * layout 4: layout 2's tiles and weight copy with each tile cut into 16 K
+ *           chunks of S steps (K = 512 * S, S in {19, 8, 5}); the chunks of all
+ *           tiles are dealt out in order, one per wavefront, `rows` = 10 per
+ *           workgroup, so every workgroup streams the same bytes; the last of
+ *           a tile's workgroups adds their fp32 partial tiles in workgroup
+ *           order (deterministic) and runs the epilogue. F32, BF16 or RESID, no
+ *           NORM. part is its scratch (part_len >= ko_gemv_argmax_scratch(N, 4,
+ *           10, 0)), with the rules of layout 3's.
  * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
             float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,
@@ -265,7 +273,8 @@ int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float*
 
 /* Number of fp32 scratch elements ko_gemv needs for N columns with this launch
  * configuration: the ARGMAX partials (epi 4) of layouts 0-2, or layout 3's
- * slots and counters (rows > 1). A size, not a status; -1 for bad arguments.
+ * (rows > 1) and layout 4's slots and counters. A size, not a status; -1 for
+ * bad arguments.
  * Helper of ko_gemv, no reference counterpart. */
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves);
 

@@ -263,7 +263,7 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 long long parts_for(int N, int layout, int rows, int waves) {
   if (layout == 0) return (N + rows - 1) / rows;
   if (layout == 2) return mfma_grid(N, rows);
-  if (layout != 1 || waves < 1) return 0;  // layout 3 has no ARGMAX partials
+  if (layout != 1 || waves < 1) return 0;  // layouts 3 and 4 have no ARGMAX partials
   const long long units = (N + rows - 1) / rows;
   return ((units + waves - 1) / waves) * waves;
 }
@@ -293,6 +293,10 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
     if (norm && rows > 1 && !ss) return KO_ENOTSUP;
     if (norm && ks_steps(K, rows) != 20) return KO_ENOTSUP;
     if (rows > 1 && (!part || !al16(part) || part_len < ks_scratch(N, rows))) return KO_ERANGE;
+  } else if (layout == 4) {
+    if (norm || epi == EPI_ARGMAX || epi == EPI_SWIGLU || rows != SK_W || !sk_steps(K))
+      return KO_ENOTSUP;
+    if (!part || !al16(part) || part_len < sk_scratch(N)) return KO_ERANGE;
   } else {
     return KO_EINVAL;
   }
@@ -332,8 +336,11 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
       st = launch_layout1(a, epi, norm != 0, rows, waves, s);
     else if (layout == 2)
       st = launch_layout2(a, epi, norm != 0, rows, s);
-    else
+    else if (layout == 3)
       st = launch_layout3(a, epi, norm != 0, rows, reinterpret_cast<int*>(part),
+                          part + ((N + 15) / 16 + 63) / 64 * 64, s);
+    else
+      st = launch_layout4(a, epi, reinterpret_cast<int*>(part),
                           part + ((N + 15) / 16 + 63) / 64 * 64, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
@@ -419,8 +426,9 @@ int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, vo
 // fp32 scratch elements ko_gemv needs for EPI 4 (ARGMAX) with this layout
 // (a size, not a status; -1 for bad arguments).
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
-  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 3) return -1;
+  if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 4) return -1;
   if (layout == 3) return rows > 1 ? ks_scratch(N, rows) : 0;
+  if (layout == 4) return sk_scratch(N);
   return 2LL * 16 * parts_for(N, layout, rows, waves);
 }
 

@@ -1,6 +1,6 @@
-// Launchers of the four GEMV layouts, compiled in their own sources
-// (gemv_block.hip: layout 0; gemv_wave.hip: layout 1; gemv_mfma.hip: layouts 2
-// and 3) and called
+// Launchers of the five GEMV layouts, compiled in their own sources
+// (gemv_block.hip: layout 0; gemv_wave.hip: layout 1; gemv_mfma.hip: layouts 2,
+// 3 and 4) and called
 // by the C entry points in gemv.hip, plus the shape rules those entry points
 // validate against.
 #pragma once
@@ -12,6 +12,9 @@ namespace ko {
 constexpr int LDS_X_BYTES = 40960;  // layout 1: normalised x staged for the workgroup (M*K*2)
 constexpr int MFMA_CUS = 256;       // MI355X compute units: layout-2 grid of at most 256 x rows
 constexpr int KS_MAX = 32;          // layout 3: slices per tile
+constexpr int SK_W = 10;            // layout 4: wavefronts (chunks) per workgroup
+constexpr int SK_CPT = 16;          // layout 4: chunks per tile
+constexpr int SK_SPT = 3;           // layout 4: workgroups a tile's chunks can span (SK_W < SK_CPT)
 
 // layout 0: `rows` (4, 8; 16 for M <= 2) columns per 256-thread workgroup
 int launch_layout0(const GemvArgs& a, int epi, bool norm, int rows, hipStream_t s);
@@ -22,6 +25,8 @@ int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_
 // layout 3: MFMA tiles with the K range cut into `slices`
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s);
+// layout 4: MFMA tiles cut into SK_CPT chunks dealt out SK_W per workgroup
+int launch_layout4(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s);
 
 // Workgroups of the layout-2 grid: at most MFMA_CUS * per_cu, and of those the
 // fewest that keep the most tiles per workgroup at its minimum, so every
@@ -58,6 +63,20 @@ inline int ks_steps(int K, int slices) {
 inline long long ks_scratch(int N, int slices) {
   const long long T = (N + 15) / 16;
   return ((T + 63) / 64) * 64 + T * slices * 2 * 256;
+}
+
+// Layout 4: steps per chunk (K = 512 S; 0: unsupported), the grid, and the
+// scratch (fp32 elements): the tiles' arrival counters as in layout 3, then
+// SK_SPT 16 x 16 fp32 slots per tile.
+inline int sk_steps(int K) {
+  if (K % (32 * SK_CPT)) return 0;
+  const int S = K / (32 * SK_CPT);
+  return (S == 19 || S == 8 || S == 5) ? S : 0;
+}
+inline int sk_grid(int N) { return ((N + 15) / 16 * SK_CPT + SK_W - 1) / SK_W; }
+inline long long sk_scratch(int N) {
+  const long long T = (N + 15) / 16;
+  return ((T + 63) / 64) * 64 + T * SK_SPT * 256;
 }
 
 }  // namespace ko

@@ -63,7 +63,12 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   // NORM gain) is loaded first, then the first tile's weights: loads return in
   // issue order, so the prologue runs while the weights stream. The weights
   // stay issued there (the scheduler would otherwise sink the loads next to
-  // their MFMAs to save registers).
+  // their MFMAs to save registers). With NORM the compiler turns the masked x
+  // loads into branches and waits for the second one before issuing the rest,
+  // so the weights go out one memory round trip after x. Measured at 16 rows,
+  // that order beats issuing everything at once (unmasked loads: qkv 10.5
+  // against 10.3 us, gate/up 20.7 against 20.1) and an explicit wait for all
+  // of x and the gain before the weights (10.4 / 20.7).
   constexpr bool NW_EARLY = NORM && S <= 10;
   bf16x8 xa[S];
   {
@@ -321,6 +326,119 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
   }
 }
 
+// layout 4: the layout-2 weight tiles cut into SK_CPT chunks of S K steps
+// (K = 512 S), the T * SK_CPT chunks dealt out in order to workgroups of
+// SK_W wavefronts, one chunk per wavefront ("stream-K"). Every CU then gets
+// the same number of chunks, where layout 3's (tile, slice) workgroups leave
+// some CUs one workgroup more than others (16 rows, down projection: 640
+// workgroups of 4 wavefronts, and the time follows the CUs that hold 3). A
+// workgroup's chunks span at most two tiles: its wavefronts' partial tiles are
+// summed per tile through LDS (thread group 0 for the first tile, group 1 for
+// the second), each sum goes to the tile's slot for this workgroup with
+// device-coherent stores, and the workgroup counts itself on the tile's
+// counter. The last of a tile's (2 or 3) workgroups adds the slots in
+// workgroup order (the result does not depend on the arrival order), re-arms
+// the counter and runs the epilogue.
+template <int EPI, int S, int PD>
+__global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int* __restrict__ ctr,
+                                                                float* __restrict__ slots) {
+  static_assert(EPI != EPI_ARGMAX && EPI != EPI_SWIGLU, "layout 4: F32, BF16 or RESID");
+  static_assert(PD <= S, "the weight ring holds at most the chunk");
+  __shared__ float s_c[SK_W][16][17];
+  __shared__ int s_prev[2];
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, mr = a.mrows;
+  const int T = (N + 15) / 16, KS = K / 32, nch = T * SK_CPT;
+  const int c0 = blockIdx.x * SK_W;              // this workgroup's first chunk
+  const int c = c0 + wv;                          // this wavefront's chunk
+  const bool live = c < nch;
+  const int cl = live ? c : nch - 1;              // past the end: a valid chunk, result unused
+  const int tile = cl / SK_CPT;
+  const int sb = (cl - tile * SK_CPT) * S;        // its first K step
+  const int kw0 = sb * 32 + 8 * g;
+  const bool mok = col < mr;
+
+  const uint16_t* wlane = a.w + 8 * lane;
+  uint4 wb[PD];
+  auto issue = [&](int st, int slot) {
+    wb[slot] = ldg16_stream(wlane + ((long long)tile * KS + sb + st) * 512);
+  };
+  bf16x8 xa[S];
+  {
+    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+    uint4 xr[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) xr[st] = mok ? ldg16(xrow + 32 * st) : make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // x ahead of the weights
+#pragma unroll
+    for (int st = 0; st < PD; ++st) issue(st, st);
+    __builtin_amdgcn_sched_barrier(0);  // the whole ring issued here
+#pragma unroll
+    for (int st = 0; st < S; ++st) xa[st] = __builtin_bit_cast(bf16x8, xr[st]);
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+    const int slot = st % PD;
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], __builtin_bit_cast(bf16x8, wb[slot]), acc,
+                                                  0, 0, 0);
+    if (st + PD < S) issue(st + PD, slot);
+  }
+  // C lane layout: column col, rows 4g + i.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_c[wv][4 * g + i][col] = acc[i];
+  __syncthreads();
+
+  const int clast = (c0 + SK_W < nch ? c0 + SK_W : nch) - 1;
+  const int t0 = c0 / SK_CPT, t1 = clast / SK_CPT;  // t1 - t0 <= 1 (SK_W < SK_CPT)
+  const int gi = t >> 8;                            // thread group: tile t0 + gi
+  const int tt = t0 + gi;
+  const bool grp = gi <= t1 - t0;                   // uniform per wavefront
+  const int r = t & 255, m = r >> 4, j = r & 15, n = tt * 16 + j;
+  float tot = 0.f;
+  int nwg = 1, sl = 0;
+  if (grp) {
+    const int v0 = (tt * SK_CPT > c0 ? tt * SK_CPT : c0) - c0;
+    const int v1 = ((tt + 1) * SK_CPT < clast + 1 ? (tt + 1) * SK_CPT : clast + 1) - c0;
+    for (int v = v0; v < v1; ++v) tot += s_c[v][m][j];
+    const int first = tt * SK_CPT / SK_W;
+    nwg = (tt * SK_CPT + SK_CPT - 1) / SK_W - first + 1;
+    sl = blockIdx.x - first;
+    if (nwg > 1)
+      __hip_atomic_store(slots + ((long long)tt * SK_SPT + sl) * 256 + r, tot, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's slot store is performed
+  __syncthreads();
+  if (grp && r == 0 && nwg > 1)
+    s_prev[gi] = __hip_atomic_fetch_add(ctr + tt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (!grp) return;
+  if (nwg > 1) {
+    if (s_prev[gi] != nwg - 1) return;
+    const float* base = slots + (long long)tt * SK_SPT * 256 + r;
+    float v[SK_SPT];
+#pragma unroll
+    for (int q = 0; q < SK_SPT; ++q)
+      v[q] = q < nwg ? __hip_atomic_load(base + q * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : 0.f;
+    tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < SK_SPT; ++q)
+      if (q < nwg) tot += v[q];
+    if (r == 0) __hip_atomic_store(ctr + tt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool ok = m < mr && n < N;
+  float h2 = 0.f;
+  if (ok) h2 = epilogue<EPI>(a, m, n, tot, 0.f);
+  if constexpr (EPI == EPI_RESID) {
+    if (a.ss_out) {
+      h2 = row_sum16(h2);
+      if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+    }
+  }
+}
+
 template <int S, int PD, int WPG>
 int launch_mfma_s(const GemvArgs& a, int epi, bool norm, int grid, hipStream_t s) {
   const int ntiles = (a.N + 15) / 16;
@@ -409,6 +527,33 @@ int launch_mfma_ks(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, 
 }
 
 
+template <int S, int PD>
+int launch_mfma_sk_s(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
+  const dim3 grid(sk_grid(a.N));
+  switch (epi) {
+    case EPI_F32:
+      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_F32, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
+      break;
+    case EPI_BF16:
+      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_BF16, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_RESID, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
+      break;
+  }
+  return KO_LAUNCH_STATUS();
+}
+
+int launch_mfma_sk(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
+  switch (sk_steps(a.K)) {
+    case 19: return launch_mfma_sk_s<19, 10>(a, epi, ctr, slots, s);
+    case 8: return launch_mfma_sk_s<8, 8>(a, epi, ctr, slots, s);
+    case 5: return launch_mfma_sk_s<5, 5>(a, epi, ctr, slots, s);
+    default: return KO_ENOTSUP;
+  }
+}
+
+
 }  // namespace
 
 namespace ko {
@@ -420,6 +565,10 @@ int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s) {
   return launch_mfma_ks(a, epi, norm, slices, ctr, slots, s);
+}
+
+int launch_layout4(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
+  return launch_mfma_sk(a, epi, ctr, slots, s);
 }
 
 }  // namespace ko

@@ -19,10 +19,12 @@ Additions of this backend:
 ``cfg`` is an opaque tuple ``(layout, rows, waves)``: layout 0 gives each
 256-thread workgroup ``rows`` output columns (any M); layout 1 gives each
 wavefront ``rows`` columns with ``waves`` wavefronts per workgroup sharing the
-normalised input through LDS (M <= 4); layouts 2 and 3 put 2..16 rows on MFMA
-tiles and read a tiled copy of the weights (``tile_weights``), layout 3 with
-the K range of a tile cut into ``rows`` slices merged by the tile's last slice
-(no atomics on the output, so the F32 epilogue is a plain store).
+normalised input through LDS (M <= 4); layouts 2, 3 and 4 put 2..16 rows on
+MFMA tiles and read a tiled copy of the weights (``tile_weights``), layout 3 with
+the K range of a tile cut into ``rows`` slices merged by the tile's last slice,
+layout 4 with each tile cut into 16 K chunks dealt out 10 per workgroup and
+merged by the tile's last workgroup (no atomics on the output in either, so the
+F32 epilogue is a plain store).
 ``allow_split`` is accepted for signature compatibility.
 
 Drop-in rule for the tiled layouts: the default configuration (``cfg`` before
@@ -45,8 +47,8 @@ EPI_F32, EPI_BF16, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3, 4
 
 
 def uses_tiled(cfg):
-    """Layouts 2 and 3 (MFMA) read the tile_weights copy of the weights."""
-    return cfg[0] in (2, 3)
+    """Layouts 2, 3 and 4 (MFMA) read the tile_weights copy of the weights."""
+    return cfg[0] in (2, 3, 4)
 
 
 def is_tiled(w):
@@ -86,6 +88,13 @@ class Gemv:
                 out.append(s)
         return [s for s in out if s == 1 and self.K == 2560] if self.norm else out
 
+    def sk_ok(self):
+        """Layout 4 (MFMA tiles cut into 16 chunks of S steps, dealt out 10 per
+        workgroup; gemv.hip, sk_steps): K = 512 * S with S in {19, 8, 5}, no NORM,
+        F32, BF16 or RESID."""
+        return (not self.norm and self.epi in (EPI_F32, EPI_BF16, EPI_RESID)
+                and self.K % 512 == 0 and self.K // 512 in (19, 8, 5))
+
     def candidates(self):
         """Launch configurations, the default first. The default is always a
         row-major layout, so an untuned Gemv runs on the weights the caller holds.
@@ -93,10 +102,13 @@ class Gemv:
         serves every batch up to 16 rows per launch with VALU dot products;
         layout 2 puts 2..16 rows on MFMA (``(2, per_cu, 0)``: a persistent grid
         of at most 256 x per_cu workgroups, the fewest that keep the most tiles
-        per workgroup at its minimum) and layout 3 splits its tiles' K range."""
+        per workgroup at its minimum), layout 3 splits its tiles' K range and
+        layout 4 (``(4, 10, 0)``) deals the tiles' 16 K chunks out 10 per
+        workgroup."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
         mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
+        mfma += [(4, 10, 0)] if self.M >= 2 and self.sk_ok() else []
         if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):
             per_wave = (4, 2, 1) if self.N >= 32768 else (1, 2, 4)
             for rows in per_wave:
@@ -108,9 +120,9 @@ class Gemv:
         return out + mfma
 
     def _scratch(self, device, cfg):
-        """fp32 scratch of the ARGMAX partials or of layout 3's slots and arrival
-        counters (allocated zeroed: the counters start at zero and every launch
-        leaves them there)."""
+        """fp32 scratch of the ARGMAX partials or of layout 3's and 4's slots and
+        arrival counters (allocated zeroed: the counters start at zero and every
+        launch leaves them there)."""
         n = _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg)
         if self._part is None or self._part.device != device or self._part.numel() < n:
             self._part = torch.zeros(max(n, 2), dtype=torch.float32, device=device)
@@ -189,7 +201,7 @@ class Gemv:
                       "ring host must be a pinned contiguous int64 [R, M] CPU tensor")
                 _check(ctr, "ring counter", torch.int32, (M,))
         part = (self._scratch(x.device, (layout, rows, waves))
-                if epi == EPI_ARGMAX or (layout == 3 and rows > 1) else None)
+                if epi == EPI_ARGMAX or (layout == 3 and rows > 1) or layout == 4 else None)
         if epi == EPI_ARGMAX and (rope is not None or ring is not None):
             cos, sin, rope_out = rope if rope is not None else (None, None, None)
             host, ctr = ring if ring is not None else (None, None)
@@ -238,7 +250,7 @@ class Gemv:
         # the scratch is sized for every candidate before any graph captures it:
         # the graphs are replayed after all captures
         for cfg in self.candidates():
-            if ((self.epi == EPI_ARGMAX or cfg[0] == 3)
+            if ((self.epi == EPI_ARGMAX or cfg[0] in (3, 4))
                     and _lib.lib().ko_gemv_argmax_scratch(self.N, *cfg) > 0):
                 self._scratch(dev, cfg)
         graphs = []

@@ -86,7 +86,7 @@ def test_gemv_host_path_of_every_layout_without_gpu(libpath):
     P = 1 << 20
     for K, layout, rows, waves in [(4096, 3, 4, 0), (4096, 3, 8, 0), (9728, 3, 4, 0),
                                    (9728, 3, 19, 0), (2560, 3, 1, 0), (2560, 2, 1, 0),
-                                   (2560, 0, 8, 0)]:
+                                   (2560, 0, 8, 0), (9728, 4, 10, 0), (4096, 4, 10, 0)]:
         st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 2, 2560, K,
                        1, 0, 0, layout, rows, waves, 1e-6, None)
         assert st > 0, (K, layout, rows, st)   # a HIP status from the launch, not a host error
@@ -97,3 +97,11 @@ def test_gemv_host_path_of_every_layout_without_gpu(libpath):
     st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 16, 2, 2560, 4096, 1, 0,
                    0, 3, 4, 0, 1e-6, None)
     assert st == -34   # layout 3 scratch too small
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 16, 2, 2560, 4096, 1, 0,
+                   0, 4, 10, 0, 1e-6, None)
+    assert st == -34   # layout 4 scratch too small
+    for K, norm, rows in [(2560, 1, 10), (4096, 0, 8), (2560 + 512, 0, 10)]:
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 2, 2560, K,
+                       1, norm, 0, 4, rows, 0, 1e-6, None)
+        assert st == -95, (K, norm, rows, st)   # layout 4: no NORM, 10 waves, K = 512 S
+    assert h.ko_gemv_argmax_scratch(2560, 4, 10, 0) == 192 + 160 * 3 * 256

@@ -186,9 +186,10 @@ def test_gemv_epilogues(dev, M, cfg):
 def test_gemv_split_k_layout(dev, M):
     """Layout 3 (MFMA tiles, K cut into slices merged by the last workgroup of
     each tile, in slice order) for every Qwen3-4B projection and every slice
-    count it takes, against the oracle; bit-identical on a second call and on
-    graph replays (the arrival counters re-arm); M = 20 runs as 16 + 4 rows on
-    the same counters."""
+    count it takes, and layout 4 (each tile's 16 K chunks dealt out 10 per
+    workgroup, merged in workgroup order) for the projections it takes, against
+    the oracle; bit-identical on a second call and on graph replays (the arrival
+    counters re-arm); M = 20 runs as 16 + 4 rows on the same counters."""
     _, gemv = K()
     g = _g(dev, 50 + M)
     nw = (1 + 0.1 * torch.randn(2560, device=dev, generator=g)).to(BF)
@@ -223,9 +224,10 @@ def test_gemv_split_k_layout(dev, M):
     for name, op, xin, Wt, extra, out_name, N, want in cases:
         slices = op.ks_slices()
         assert slices, f"{name}: layout 3 offers no slice count"
-        for sl in slices:
+        cfgs = [(3, sl, 0) for sl in slices] + ([(4, 10, 0)] if op.sk_ok() else [])
+        for cfg in cfgs:
+            sl = cfg[1] if cfg[0] == 3 else "sk"
             seen.add((name, sl))
-            cfg = (3, sl, 0)
 
             def run():
                 kw = {}
@@ -263,7 +265,8 @@ def test_gemv_split_k_layout(dev, M):
                 gr.replay()
                 torch.cuda.synchronize()
                 assert torch.equal(r3, r1), f"{name} slices {sl}: graph replay differs"
-    assert {("o", 4), ("o", 8), ("down", 4), ("down", 19), ("qkv", 1), ("gu", 1)} <= seen
+    assert {("o", 4), ("o", 8), ("down", 4), ("down", 19), ("qkv", 1), ("gu", 1), ("o", "sk"),
+            ("down", "sk")} <= seen
 
 
 @pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (3, (0, 8, 0)),
