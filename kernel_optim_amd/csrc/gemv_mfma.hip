@@ -76,6 +76,11 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
     uint4 xr[S], nwv[NW_EARLY ? S : 1];
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    // the caller's row sums, loaded with x: a load issued after the weights
+    // would make the norm wait for every weight step (loads return in order)
+    float ssv = 0.f;
+    if constexpr (NORM)
+      if (a.ss) ssv = a.ss[mok ? col : 0];
     if constexpr (NW_EARLY) {
 #pragma unroll
       for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
@@ -87,7 +92,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
     if constexpr (NORM) {
       float rstd;
       if (a.ss) {
-        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+        rstd = mok ? rsqrtf(ssv / (float)K + a.eps) : 0.f;
       } else {
         float sq = 0.f;
 #pragma unroll
@@ -228,7 +233,9 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
     uint4 xr[S], nwv[NORM ? S : 1];
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    float ssv = 0.f;  // the caller's row sums, loaded with x (as in layout 2)
     if constexpr (NORM) {
+      if (a.ss) ssv = a.ss[mok ? col : 0];
 #pragma unroll
       for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
     }
@@ -241,7 +248,7 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
     if constexpr (NORM) {
       float rstd;
       if (a.ss) {
-        rstd = mok ? rsqrtf(a.ss[col] / (float)K + a.eps) : 0.f;
+        rstd = mok ? rsqrtf(ssv / (float)K + a.eps) : 0.f;
       } else {  // one slice: the KSW wavefronts hold the whole row
         float sq = 0.f;
 #pragma unroll
