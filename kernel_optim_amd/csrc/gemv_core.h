@@ -54,10 +54,20 @@ __device__ __forceinline__ float sq8(const uint4& v) {
   return s;
 }
 
+// RESID: the residual element (m, n) as raw bf16, loaded ahead of the work
+// that produces its sum so the epilogue does not wait a memory round trip for
+// it. Rows past mrows and columns past N read a valid element (unused).
+__device__ __forceinline__ uint16_t resid_load(const GemvArgs& a, int m, int n) {
+  const int mm = m < a.mrows ? m : 0, nn = n < a.N ? n : a.N - 1;
+  return a.h[(long long)mm * a.N + nn];
+}
+
 // Epilogue for one finished output element (m, n) with full sums (tot, tot2).
-// Returns the bf16-rounded new residual squared (RESID) or 0.
+// Returns the bf16-rounded new residual squared (RESID) or 0. RESID takes the
+// residual from `hres` (resid_load) when given, else loads it here.
 template <int EPI>
-__device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float tot, float tot2) {
+__device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float tot, float tot2,
+                                          const uint16_t* hres = nullptr) {
   const long long o = (long long)m * a.N + n;
   if constexpr (EPI == EPI_F32) {
     float* y = static_cast<float*>(a.y);
@@ -70,7 +80,7 @@ __device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float
     const float s = round_bf16(g / (1.0f + expf(-g)));
     static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(s * u);
   } else if constexpr (EPI == EPI_RESID) {
-    const float hn = round_bf16(bf16_to_f32(a.h[o]) + round_bf16(tot));
+    const float hn = round_bf16(bf16_to_f32(hres ? *hres : a.h[o]) + round_bf16(tot));
     a.h[o] = f32_to_bf16(hn);
     return hn * hn;
   } else {  // ARGMAX: logits only; the selection is done by the caller
@@ -119,6 +129,13 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
       if constexpr (NORM) nwr[j] = ldg16(a.nw + 8 * c);
     }
   };
+  static_assert(M * R <= GEMV_NT, "one epilogue element per thread");
+  // RESID: this thread's residual element, issued before the weights
+  uint16_t hpre = 0;
+  if constexpr (EPI == EPI_RESID) {
+    const int ti = t < M * R ? t : 0;
+    hpre = resid_load(a, ti / R, n0 + ti % R);
+  }
   if constexpr (!XCOH) load_x();
   uint4 w[CPT][NW];
 #pragma unroll
@@ -201,7 +218,7 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
     }
     const bool ok = m < mr && n < N;
     float h2 = 0.f;
-    if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+    if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2, &hpre);  // idx == t: M * R <= GEMV_NT
     if constexpr (EPI == EPI_RESID) s_h2[idx] = h2;
     if constexpr (EPI == EPI_ARGMAX)
       s_best[idx] = make_float2(ok ? round_bf16(tot) : -INFINITY,

@@ -38,6 +38,7 @@ template <int EPI, bool NORM, int S, int PD, int WPG>
 __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int ntiles) {
   static_assert(S % PD == 0, "the weight ring must tile the K steps");
   constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr bool HPRE = EPI == EPI_RESID && S <= 16;  // residual loaded ahead (registers)
   __shared__ float s_c[WPG][NW][16][17];
   __shared__ float s_sq[WPG][16];
 
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   int bi = 0x7fffffff;
   // The wavefronts' partial tiles summed through LDS, then the epilogue, one
   // thread per (m, n).
-  auto finish = [&](int tile, const f32x4* c) {
+  auto finish = [&](int tile, const f32x4* c, uint16_t hpre) {
     // C lane layout: column col, rows 4g + i.
 #pragma unroll
     for (int r = 0; r < NW; ++r)
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
       }
       const bool ok = m < mr && n < N;
       float h2 = 0.f;
-      if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+      if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2, HPRE ? &hpre : nullptr);
       if constexpr (EPI == EPI_RESID) {
         if (a.ss_out) {
           h2 = row_sum16(h2);
@@ -163,6 +164,11 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   // instead cost ~4.5 us of the 16-row gate/up GEMV's ~25.)
   auto run = [&](auto issue_c, int tile, int next) {
     constexpr bool ISSUE = decltype(issue_c)::value != 0;
+    // RESID: the tile's residual element of this thread, issued behind the
+    // tile's weights and ahead of the next tile's, so the epilogue finds it in
+    // (not at 38 steps per wavefront, whose registers are full)
+    uint16_t hpre = 0;
+    if constexpr (HPRE) hpre = resid_load(a, (t >> 4) & 15, tile * 16 + (t & 15));
     f32x4 c[NW];
 #pragma unroll
     for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
       if (s + PD < S) issue(tile, s + PD, slot);
       else if constexpr (ISSUE) issue(next, s + PD - S, slot);
     }
-    finish(tile, c);
+    finish(tile, c, hpre);
   };
 
   int tile = blockIdx.x;
@@ -225,6 +231,7 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
       wb[slot][r] = ldg16_stream(wlane + ((long long)(r * T + tile) * KS + sb + s) * 512);
   };
 
+  uint16_t hpre = 0;
   // x (and the NORM gain) first: loads return in issue order, so the prologue
   // then runs while the weights stream instead of after them.
   bf16x8 xa[S];
@@ -234,6 +241,8 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
     float ssv = 0.f;  // the caller's row sums, loaded with x (as in layout 2)
+    if constexpr (EPI == EPI_RESID)  // the residual, for the slice that merges
+      hpre = resid_load(a, t >> 4, tile * 16 + (t & 15));
     if constexpr (NORM) {
       if (a.ss) ssv = a.ss[mok ? col : 0];
 #pragma unroll
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
   }
   const bool ok = m < mr && n < N;
   float h2 = 0.f;
-  if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2);
+  if (ok) h2 = epilogue<EPI>(a, m, n, tot, tot2, &hpre);
   if constexpr (EPI == EPI_RESID) {
     if (a.ss_out) {
       h2 = row_sum16(h2);
@@ -370,6 +379,13 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   auto issue = [&](int st, int slot) {
     wb[slot] = ldg16_stream(wlane + ((long long)tile * KS + sb + st) * 512);
   };
+  // RESID: the residual element this thread writes if its thread group's tile
+  // (t0 + t / 256) is merged here, loaded with x
+  uint16_t hpre = 0;
+  if constexpr (EPI == EPI_RESID) {
+    const int tp = c0 / SK_CPT + (t >> 8);
+    hpre = resid_load(a, (t >> 4) & 15, (tp < T ? tp : T - 1) * 16 + (t & 15));
+  }
   bf16x8 xa[S];
   {
     const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
@@ -437,7 +453,7 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   }
   const bool ok = m < mr && n < N;
   float h2 = 0.f;
-  if (ok) h2 = epilogue<EPI>(a, m, n, tot, 0.f);
+  if (ok) h2 = epilogue<EPI>(a, m, n, tot, 0.f, &hpre);
   if constexpr (EPI == EPI_RESID) {
     if (a.ss_out) {
       h2 = row_sum16(h2);
