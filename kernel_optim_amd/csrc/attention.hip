@@ -122,9 +122,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // every unit this wave processes (lane b holds sequence b's unit count and
   // inclusive prefix).
   const bool small_b = a.B <= 64;
-  int my_n = 0, my_incl = 0, total;
+  int my_n = 0, my_incl = 0, total, my_len = 0;
   if (small_b) {
-    my_n = lane < a.B ? nunits(seq_len(a.lens, lane, a.len_off, a.cap), unit) : 0;
+    if (lane < a.B) {
+      my_len = seq_len(a.lens, lane, a.len_off, a.cap);
+      my_n = nunits(my_len, unit);
+    }
     my_incl = wave_incl_scan(my_n);
     total = readlane(my_incl, 63) * nkv;
   } else {
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (small_b) {
       b = uniform(__popcll(__ballot(my_incl <= pidx)));
       c = pidx - readlane(my_incl - my_n, b);
-      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap));
+      kv_len = readlane(my_len, b);  // lane b loaded it: no second round trip
     } else {
       locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c);
       b = uniform(b);

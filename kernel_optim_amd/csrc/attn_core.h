@@ -316,7 +316,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
   }
 
   const bool small_b = a.B <= 64;
-  int my_n = 0, my_incl = 0, total, len1 = 0;
+  int my_n = 0, my_incl = 0, total, len1 = 0, my_len = 0;  // lane b: sequence b (B <= 64)
   if (a.B == 1) {
     // one sequence: its length through a scalar load (the constant address
     // space), which waits on its own counter instead of queueing behind the
@@ -328,8 +328,8 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     total = my_incl * nkv;
   } else if (small_b) {
     if (lane < a.B) {
-      const int l = seq_len(a.lens, lane, a.len_off, a.cap, a.rep);
-      my_n = nunits(l, unit_for(l, unit, a.usplit));
+      my_len = seq_len(a.lens, lane, a.len_off, a.cap, a.rep);
+      my_n = nunits(my_len, unit_for(my_len, unit, a.usplit));
     }
     my_incl = wave_incl_scan(my_n);
     total = readlane(my_incl, 63) * nkv;
@@ -351,7 +351,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
     } else if (small_b) {
       b = uniform(__popcll(__ballot(my_incl <= pidx)));
       c = pidx - readlane(my_incl - my_n, b);
-      kv_len = uniform(seq_len(a.lens, b, a.len_off, a.cap, a.rep));
+      kv_len = readlane(my_len, b);  // lane b loaded it: no second round trip
     } else {
       locate_pair(pidx, a.lens, a.len_off, a.cap, a.B, unit, b, c, a.rep);
       b = uniform(b);
