@@ -269,6 +269,45 @@ def test_gemv_split_k_layout(dev, M):
             ("down", "sk")} <= seen
 
 
+@pytest.mark.parametrize("M,N,Kd", [(5, 200, 2560), (16, 1000, 2560), (3, 2568, 4096), (16, 48, 9728)])
+def test_gemv_stream_k_shapes(dev, M, N, Kd):
+    """Layout 4 beyond the model's shapes: N not a multiple of 16 (a part-filled
+    last tile), tile counts whose chunks end inside a workgroup, grids smaller
+    than the CUs, and K = 512 S for S = 5, 8, 19; BF16, F32 and RESID against the
+    oracle, the same on a second call."""
+    _, gemv = K()
+    g = _g(dev, 110 + M + N)
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 111 + N)
+    Wt = gemv.tile_weights(W)
+    cfg = (4, 10, 0)
+    for epi in (gemv.EPI_BF16, gemv.EPI_F32, gemv.EPI_RESID):
+        op = gemv.Gemv(M, N, Kd, epi, norm=False)
+        assert op.sk_ok() and cfg in op.candidates()
+        outs = []
+        for _ in range(2):
+            if epi == gemv.EPI_RESID:
+                h = torch.randn(M, N, device=dev, generator=_g(dev, 7)).to(BF)
+                h0 = h.clone()
+                op(x, Wt, h=h, cfg=cfg)
+                outs.append(h)
+            else:
+                y = torch.empty(M, N, device=dev, dtype=torch.float32 if epi == gemv.EPI_F32 else BF)
+                op(x, Wt, y=y, cfg=cfg)
+                outs.append(y)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), epi
+        if epi == gemv.EPI_RESID:
+            want, _ = O.gemv(x.cpu(), W.cpu(), O.EPI_RESID, h=h0.cpu())
+            assert_bf16_close(outs[0].cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
+        elif epi == gemv.EPI_BF16:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_BF16)
+            assert_bf16_close(outs[0].cpu(), want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
+        else:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32)
+            torch.testing.assert_close(outs[0].cpu(), want.float(), rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (3, (0, 8, 0)),
                                    (4, (0, 4, 0)), (16, (0, 8, 0)),
                                    (3, (2, 1, 0)), (16, (2, 2, 0))])
