@@ -222,7 +222,10 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           zeros), K in {2560, 4096, 9728} (SWIGLU: 2560, 4096); a persistent
  *           grid of at most 256 * `rows` (1, 2 or 4) workgroups, the fewest
  *           that keep the most tiles per workgroup at its minimum (384 tiles:
- *           192 workgroups of 2). w must be in the tiled
+ *           192 workgroups of 2). `waves` 0, or 2 for two row tiles: M <= 32
+ *           per launch slice, each weight load feeding both tiles (K in
+ *           {2560, 4096}, SWIGLU 2560; a last slice of <= 16 rows runs on one
+ *           tile). w must be in the tiled
  *           layout written by ko_gemv_tile (for SWIGLU: the gate rows tiled,
  *           then the up rows tiled, each padded to a multiple of 16 rows).
  * layout 3: layout 2's tiles and weight copy with the K range of a tile cut

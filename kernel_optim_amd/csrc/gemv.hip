@@ -287,7 +287,8 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
     if (norm && (long long)M * K * 2 > LDS_X_BYTES) return KO_ENOTSUP;
   } else if (layout == 2) {
     if (rows != 1 && rows != 2 && rows != 4) return KO_ENOTSUP;
-    if (!mfma_supported(K, epi)) return KO_ENOTSUP;
+    if (waves != 0 && waves != 2) return KO_ENOTSUP;  // row tiles: 0 (one) or 2
+    if (!mfma_supported(K, epi, waves == 2 ? 2 : 1)) return KO_ENOTSUP;
   } else if (layout == 3) {
     if (epi == EPI_ARGMAX || !ks_steps(K, rows)) return KO_ENOTSUP;
     if (norm && rows > 1 && !ss) return KO_ENOTSUP;
@@ -300,7 +301,7 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
   } else {
     return KO_EINVAL;
   }
-  const int mstep = layout == 1 ? 4 : 16;
+  const int mstep = mstep_for(layout, waves);
   const long long nparts = parts_for(N, layout, rows, waves);
   if (epi == EPI_ARGMAX) {
     if (!ids || !part) return KO_EINVAL;
@@ -335,7 +336,7 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
     else if (layout == 1)
       st = launch_layout1(a, epi, norm != 0, rows, waves, s);
     else if (layout == 2)
-      st = launch_layout2(a, epi, norm != 0, rows, s);
+      st = launch_layout2(a, epi, norm != 0, rows, waves == 2 && mr > 16 ? 2 : 1, s);
     else if (layout == 3)
       st = launch_layout3(a, epi, norm != 0, rows, reinterpret_cast<int*>(part),
                           part + ((N + 15) / 16 + 63) / 64 * 64, s);
@@ -429,7 +430,7 @@ long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
   if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 4) return -1;
   if (layout == 3) return rows > 1 ? ks_scratch(N, rows) : 0;
   if (layout == 4) return sk_scratch(N);
-  return 2LL * 16 * parts_for(N, layout, rows, waves);
+  return 2LL * mstep_for(layout, waves) * parts_for(N, layout, rows, waves);
 }
 
 }  // extern "C"

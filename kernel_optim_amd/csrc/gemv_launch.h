@@ -20,8 +20,9 @@ constexpr int SK_SPT = 3;           // layout 4: workgroups a tile's chunks can 
 int launch_layout0(const GemvArgs& a, int epi, bool norm, int rows, hipStream_t s);
 // layout 1: `rw` columns per wavefront, `wpb` wavefronts per workgroup
 int launch_layout1(const GemvArgs& a, int epi, bool norm, int rw, int wpb, hipStream_t s);
-// layout 2: MFMA tiles, a persistent grid of at most MFMA_CUS * per_cu workgroups
-int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s);
+// layout 2: MFMA tiles, a persistent grid of at most MFMA_CUS * per_cu workgroups;
+// mt row tiles of 16 rows of x per weight pass (1, or 2 for K <= 4096)
+int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, int mt, hipStream_t s);
 // layout 3: MFMA tiles with the K range cut into `slices`
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s);
@@ -44,9 +45,17 @@ inline int mfma_grid(int N, int per_cu) {
 }
 
 // K = 32 * S * WPG: S steps of 32 per wavefront, WPG wavefronts splitting K.
-// SWIGLU (two weight tiles) needs K <= 4096 to keep its registers.
-inline bool mfma_supported(int K, int epi) {
+// SWIGLU (two weight tiles) needs K <= 4096 to keep its registers; 32 rows
+// (two row tiles of x) need K <= 4096, SWIGLU K = 2560.
+inline bool mfma_supported(int K, int epi, int mt = 1) {
+  if (mt == 2) return K == 2560 || (K == 4096 && epi != EPI_SWIGLU);
   return K == 2560 || K == 4096 || (K == 9728 && epi != EPI_SWIGLU);
+}
+
+// Rows of x per launch of a layout: 4 (layout 1), 32 (layout 2 with two row
+// tiles, waves == 2), else 16.
+inline int mstep_for(int layout, int waves) {
+  return layout == 1 ? 4 : (layout == 2 && waves == 2) ? 32 : 16;
 }
 
 // Steps per wavefront of layout 3 for K and a slice count (0: unsupported):

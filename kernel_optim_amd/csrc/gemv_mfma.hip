@@ -34,19 +34,21 @@ struct IntC {
   static constexpr int value = V;
 };
 
-template <int EPI, bool NORM, int S, int PD, int WPG>
+template <int EPI, bool NORM, int S, int PD, int WPG, int MT = 1>
 __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int ntiles) {
   static_assert(S % PD == 0, "the weight ring must tile the K steps");
+  static_assert(MT == 1 || (MT == 2 && WPG * 64 >= 512), "16 or 32 rows of x");
   constexpr int NW = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr bool HPRE = EPI == EPI_RESID && S <= 16;  // residual loaded ahead (registers)
-  __shared__ float s_c[WPG][NW][16][17];
-  __shared__ float s_sq[WPG][16];
+  __shared__ float s_c[WPG][NW][16 * MT][17];
+  __shared__ float s_sq[WPG][16 * MT];
 
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, mr = a.mrows;
   const int G = gridDim.x;
   const int kw0 = wv * (32 * S) + 8 * g;  // this lane's first k (step s adds 32 s)
   const bool mok = col < mr;               // A row m = col exists
+  const bool mok2 = col + 16 < mr;         // MT = 2: the second row tile's row col + 16
 
   // Ring of PD weight steps in flight. The weights are in the tiled layout
   // (ko_gemv_tile): the B operand of (tile, step) is one 1 KiB block with lane
@@ -72,16 +74,26 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   // of x and the gain before the weights (10.4 / 20.7).
   constexpr bool NW_EARLY = NORM && S <= 10;
   bf16x8 xa[S];
+  bf16x8 xa2[MT > 1 ? S : 1];  // MT = 2: rows 16..31 of x, the A operand of a second MFMA
   {
     const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
-    uint4 xr[S], nwv[NW_EARLY ? S : 1];
+    uint4 xr[S], nwv[NW_EARLY ? S : 1], xr2[MT > 1 ? S : 1];
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = mok ? ldg16(xrow + 32 * s) : make_uint4(0, 0, 0, 0);
+    if constexpr (MT > 1) {
+      const uint16_t* xrow2 = a.x + (long long)(mok2 ? col + 16 : 0) * K + kw0;
+#pragma unroll
+      for (int s = 0; s < S; ++s) xr2[s] = mok2 ? ldg16(xrow2 + 32 * s) : make_uint4(0, 0, 0, 0);
+    }
     // the caller's row sums, loaded with x: a load issued after the weights
     // would make the norm wait for every weight step (loads return in order)
-    float ssv = 0.f;
-    if constexpr (NORM)
-      if (a.ss) ssv = a.ss[mok ? col : 0];
+    float ssv = 0.f, ssv2 = 0.f;
+    if constexpr (NORM) {
+      if (a.ss) {
+        ssv = a.ss[mok ? col : 0];
+        if constexpr (MT > 1) ssv2 = a.ss[mok2 ? col + 16 : 0];
+      }
+    }
     if constexpr (NW_EARLY) {
 #pragma unroll
       for (int s = 0; s < S; ++s) nwv[s] = ldg16(a.nw + kw0 + 32 * s);
@@ -91,20 +103,34 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
     for (int s = 0; s < PD; ++s) issue(blockIdx.x, s, s);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) {
-      float rstd;
+      float rstd, rstd2 = 0.f;
       if (a.ss) {
         rstd = mok ? rsqrtf(ssv / (float)K + a.eps) : 0.f;
+        if constexpr (MT > 1) rstd2 = mok2 ? rsqrtf(ssv2 / (float)K + a.eps) : 0.f;
       } else {
         float sq = 0.f;
 #pragma unroll
         for (int s = 0; s < S; ++s) sq += sq8(xr[s]);
         sq = sum_xor32(sum_xor16(sq));  // the 4 lane groups of row m
         if (g == 0) s_sq[wv][col] = sq;
+        if constexpr (MT > 1) {
+          float sq2 = 0.f;
+#pragma unroll
+          for (int s = 0; s < S; ++s) sq2 += sq8(xr2[s]);
+          sq2 = sum_xor32(sum_xor16(sq2));
+          if (g == 0) s_sq[wv][16 + col] = sq2;
+        }
         __syncthreads();
         float tot = 0.f;
 #pragma unroll
         for (int w = 0; w < WPG; ++w) tot += s_sq[w][col];
         rstd = rsqrtf(tot / (float)K + a.eps);
+        if constexpr (MT > 1) {
+          float tot2 = 0.f;
+#pragma unroll
+          for (int w = 0; w < WPG; ++w) tot2 += s_sq[w][16 + col];
+          rstd2 = rsqrtf(tot2 / (float)K + a.eps);
+        }
       }
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -112,24 +138,35 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
         if constexpr (NW_EARLY) w = nwv[s];
         else w = ldg16(a.nw + kw0 + 32 * s);
         xr[s] = norm8(xr[s], w, rstd);
+        if constexpr (MT > 1) xr2[s] = norm8(xr2[s], w, rstd2);
       }
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) xa[s] = __builtin_bit_cast(bf16x8, xr[s]);
+    if constexpr (MT > 1) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) xa2[s] = __builtin_bit_cast(bf16x8, xr2[s]);
+    }
   }
 
   float bv = -INFINITY;  // ARGMAX: running best of row t / 16 (threads with t % 16 == 0)
   int bi = 0x7fffffff;
   // The wavefronts' partial tiles summed through LDS, then the epilogue, one
   // thread per (m, n).
-  auto finish = [&](int tile, const f32x4* c, uint16_t hpre) {
-    // C lane layout: column col, rows 4g + i.
+  auto finish = [&](int tile, const f32x4* c, const f32x4* c2, uint16_t hpre) {
+    // C lane layout: column col, rows 4g + i (16 + 4g + i for the second row tile).
 #pragma unroll
     for (int r = 0; r < NW; ++r)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_c[wv][r][4 * g + i][col] = c[r][i];
+    if constexpr (MT > 1) {
+#pragma unroll
+      for (int r = 0; r < NW; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_c[wv][r][16 + 4 * g + i][col] = c2[r][i];
+    }
     __syncthreads();
-    if (t < 256) {
+    if (t < 256 * MT) {
       const int m = t >> 4, j = t & 15, n = tile * 16 + j;
       float tot = 0.f, tot2 = 0.f;
 #pragma unroll
@@ -168,21 +205,29 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
     // tile's weights and ahead of the next tile's, so the epilogue finds it in
     // (not at 38 steps per wavefront, whose registers are full)
     uint16_t hpre = 0;
-    if constexpr (HPRE) hpre = resid_load(a, (t >> 4) & 15, tile * 16 + (t & 15));
-    f32x4 c[NW];
+    if constexpr (HPRE) hpre = resid_load(a, (t >> 4) & (16 * MT - 1), tile * 16 + (t & 15));
+    f32x4 c[NW], c2[MT > 1 ? NW : 1];
 #pragma unroll
     for (int r = 0; r < NW; ++r) c[r] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MT > 1) {
+#pragma unroll
+      for (int r = 0; r < NW; ++r) c2[r] = {0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int slot = s % PD;
 #pragma unroll
-      for (int r = 0; r < NW; ++r)
+      for (int r = 0; r < NW; ++r) {
         c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
                                                        c[r], 0, 0, 0);
+        if constexpr (MT > 1)  // the same weights, rows 16..31: one weight pass for 32 rows
+          c2[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa2[s], __builtin_bit_cast(bf16x8, wb[slot][r]),
+                                                          c2[r], 0, 0, 0);
+      }
       if (s + PD < S) issue(tile, s + PD, slot);
       else if constexpr (ISSUE) issue(next, s + PD - S, slot);
     }
-    finish(tile, c, hpre);
+    finish(tile, c, c2, hpre);
   };
 
   int tile = blockIdx.x;
@@ -190,7 +235,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_mfma_kernel(GemvArgs a, int nti
   if (tile < ntiles) run(IntC<0>{}, tile, tile);
   if constexpr (EPI == EPI_ARGMAX) {
     const int m = t >> 4;
-    if (t < 256 && (t & 15) == 0 && m < mr)
+    if (t < 256 * MT && (t & 15) == 0 && m < mr)
       a.part[(long long)m * a.nparts + blockIdx.x] = make_float2(bv, __int_as_float(bi));
   }
 }
@@ -462,12 +507,21 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   }
 }
 
-template <int S, int PD, int WPG>
+// Two row tiles (MT = 2) are built only where launch_mfma sends them: SwiGLU with
+// the short prefetch (PD < S, its doubled weights), every other epilogue with PD = S.
+template <int EPI, int S, int PD, int MT>
+constexpr bool mfma_built() {
+  return MT == 1 || ((EPI == EPI_SWIGLU) == (PD < S));
+}
+
+template <int S, int PD, int WPG, int MT = 1>
 int launch_mfma_s(const GemvArgs& a, int epi, bool norm, int grid, hipStream_t s) {
   const int ntiles = (a.N + 15) / 16;
-#define KO_M(NORMV, EPIV)                                                             \
-  hipLaunchKernelGGL((gemv_mfma_kernel<EPIV, NORMV, S, PD, WPG>), dim3(grid), dim3(64 * WPG), 0, \
-                     s, a, ntiles)
+#define KO_M(NORMV, EPIV)                                                              \
+  if constexpr (mfma_built<EPIV, S, PD, MT>())                                         \
+    hipLaunchKernelGGL((gemv_mfma_kernel<EPIV, NORMV, S, PD, WPG, MT>), dim3(grid),    \
+                       dim3(64 * WPG), 0, s, a, ntiles);                               \
+  else return KO_ENOTSUP
   if (norm) {
     switch (epi) {
       case EPI_F32: KO_M(true, EPI_F32); break;
@@ -490,8 +544,19 @@ int launch_mfma_s(const GemvArgs& a, int epi, bool norm, int grid, hipStream_t s
 }
 
 
-int launch_mfma(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s) {
+int launch_mfma(const GemvArgs& a, int epi, bool norm, int per_cu, int mt, hipStream_t s) {
   const int grid = mfma_grid(a.N, per_cu);
+  if (mt == 2) {  // 32 rows per weight pass: x of both row tiles in registers (K <= 4096)
+    switch (a.K) {
+      case 2560:
+        if (epi == EPI_SWIGLU) return launch_mfma_s<10, 5, 8, 2>(a, epi, norm, grid, s);
+        return launch_mfma_s<10, 10, 8, 2>(a, epi, norm, grid, s);
+      case 4096:
+        if (epi == EPI_SWIGLU) return KO_ENOTSUP;
+        return launch_mfma_s<16, 16, 8, 2>(a, epi, norm, grid, s);
+      default: return KO_ENOTSUP;
+    }
+  }
   switch (a.K) {
     case 2560: return launch_mfma_s<10, 10, 8>(a, epi, norm, grid, s);
     case 4096: return launch_mfma_s<16, 16, 8>(a, epi, norm, grid, s);
@@ -581,8 +646,8 @@ int launch_mfma_sk(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream
 
 namespace ko {
 
-int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, hipStream_t s) {
-  return launch_mfma(a, epi, norm, per_cu, s);
+int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, int mt, hipStream_t s) {
+  return launch_mfma(a, epi, norm, per_cu, mt, s);
 }
 
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,

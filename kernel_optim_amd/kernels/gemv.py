@@ -20,7 +20,8 @@ Additions of this backend:
 256-thread workgroup ``rows`` output columns (any M); layout 1 gives each
 wavefront ``rows`` columns with ``waves`` wavefronts per workgroup sharing the
 normalised input through LDS (M <= 4); layouts 2, 3 and 4 put 2..16 rows on
-MFMA tiles and read a tiled copy of the weights (``tile_weights``), layout 3 with
+MFMA tiles (layout 2 with ``waves`` = 2: 32 rows, two row tiles sharing each
+weight load) and read a tiled copy of the weights (``tile_weights``), layout 3 with
 the K range of a tile cut into ``rows`` slices merged by the tile's last slice,
 layout 4 with each tile cut into 16 K chunks dealt out 10 per workgroup and
 merged by the tile's last workgroup (no atomics on the output in either, so the
@@ -76,6 +77,12 @@ class Gemv:
         SWIGLU only up to 4096 (gemv.hip, mfma_supported)."""
         return self.K in (2560, 4096) or (self.K == 9728 and self.epi != EPI_SWIGLU)
 
+    def mfma2_ok(self):
+        """Layout 2 with two row tiles (``waves`` = 2: 32 rows of x per weight
+        pass) keeps both tiles of x in registers: K in {2560, 4096}, SWIGLU
+        K = 2560 (gemv_launch.h, mfma_supported)."""
+        return self.K == 2560 or (self.K == 4096 and self.epi != EPI_SWIGLU)
+
     def ks_slices(self):
         """K slices layout 3 takes for this projection (gemv.hip, ks_steps):
         K = 128 * S * slices with S in {20, 19, 8, 4}; NORM computes the row norms
@@ -102,11 +109,13 @@ class Gemv:
         serves every batch up to 16 rows per launch with VALU dot products;
         layout 2 puts 2..16 rows on MFMA (``(2, per_cu, 0)``: a persistent grid
         of at most 256 x per_cu workgroups, the fewest that keep the most tiles
-        per workgroup at its minimum), layout 3 splits its tiles' K range and
+        per workgroup at its minimum; ``(2, per_cu, 2)``: 32 rows per weight
+        pass, offered above 16 rows), layout 3 splits its tiles' K range and
         layout 4 (``(4, 10, 0)``) deals the tiles' 16 K chunks out 10 per
         workgroup."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
+        mfma += [(2, 2, 2), (2, 1, 2)] if self.M > 16 and self.mfma2_ok() else []
         mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
         mfma += [(4, 10, 0)] if self.M >= 2 and self.sk_ok() else []
         if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):

@@ -105,3 +105,15 @@ def test_gemv_host_path_of_every_layout_without_gpu(libpath):
                        1, norm, 0, 4, rows, 0, 1e-6, None)
         assert st == -95, (K, norm, rows, st)   # layout 4: no NORM, 10 waves, K = 512 S
     assert h.ko_gemv_argmax_scratch(2560, 4, 10, 0) == 192 + 160 * 3 * 256
+    # layout 2 with two row tiles (waves 2): 32 rows per launch slice, K in {2560, 4096}
+    for M, K, epi in [(20, 2560, 0), (40, 2560, 3), (32, 4096, 2)]:
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, M, 2560, K,
+                       epi, 0, 0, 2, 1, 2, 1e-6, None)
+        assert st > 0, (M, K, epi, st)
+    for K, epi, waves in [(9728, 1, 2), (4096, 3, 2), (2560, 1, 1), (2560, 1, 4)]:
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 20, 2560, K,
+                       epi, 0, 0, 2, 1, waves, 1e-6, None)
+        assert st == -95, (K, epi, waves, st)
+    # ARGMAX partials: 160 tiles on 160 workgroups, 16 or 32 rows each
+    assert h.ko_gemv_argmax_scratch(2560, 2, 1, 0) == 2 * 16 * 160
+    assert h.ko_gemv_argmax_scratch(2560, 2, 1, 2) == 2 * 32 * 160

@@ -182,6 +182,76 @@ def test_gemv_epilogues(dev, M, cfg):
     assert_bf16_close(y.cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
 
 
+@pytest.mark.parametrize("M", [17, 32, 40])
+@pytest.mark.parametrize("cfg", [(2, 1, 2), (2, 2, 2)])
+def test_gemv_two_row_tiles(dev, M, cfg):
+    """Layout 2 with two row tiles (32 rows of x per weight pass; M = 17 leaves
+    one row in the second tile, M = 40 runs a 32-row slice and an 8-row slice on
+    one tile). Every row equals the one-tile launch bit for bit (the same MFMA
+    steps over the same weights, the same norm sums) and the oracle within the
+    bf16 tolerance."""
+    _, gemv = K()
+    one = (2, cfg[1], 0)
+    g = _g(dev, 60 + M)
+
+    def both(op, x, w, **kw):  # the two-tile and the one-tile config, on fresh outputs
+        outs = []
+        for c in (cfg, one):
+            kk = {k: (v.clone() if k in ("y", "h", "ss_out") else v) for k, v in kw.items()}
+            op(x, w, cfg=c, **kk)
+            torch.cuda.synchronize()
+            outs.append(kk)
+        return outs
+
+    # qkv: NORM + F32, ss in-kernel and given
+    N, Kd = SHAPES["qkv"]
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    nw = (1 + 0.1 * torch.randn(Kd, device=dev, generator=g)).to(BF)
+    W = _weights(dev, N, Kd, 61)
+    Wt = gemv.tile_weights(W)
+    ss = x.float().pow(2).sum(-1)
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32, nw=nw.cpu(), ss=ss.cpu())
+    op = gemv.Gemv(M, N, Kd, gemv.EPI_F32, norm=True)
+    assert cfg in op.candidates()
+    for ss_arg in (None, ss):
+        a, b = both(op, x, Wt, y=torch.empty(M, N, device=dev), nw=nw, ss=ss_arg)
+        assert torch.equal(a["y"], b["y"])
+        torch.testing.assert_close(a["y"].cpu(), want, rtol=2e-3, atol=2e-3)
+    # o: RESID with ss_out, and BF16
+    N, Kd = SHAPES["o"]
+    xa = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    W = _weights(dev, N, Kd, 62)
+    Wt = gemv.tile_weights(W)
+    h = torch.randn(M, N, device=dev, generator=g).to(BF)
+    hr, ssr = O.gemv(xa.cpu(), W.cpu(), O.EPI_RESID, h=h.cpu())
+    op = gemv.Gemv(M, N, Kd, gemv.EPI_RESID, norm=False)
+    assert cfg in op.candidates()
+    a, b = both(op, xa, Wt, h=h, ss_out=torch.full((M,), 5.0, device=dev))
+    assert torch.equal(a["h"], b["h"])
+    assert_bf16_close(a["h"].cpu(), hr, max_frac=0.02, atol=one_ulp_at(hr))
+    torch.testing.assert_close(a["ss_out"].cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
+    op = gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)
+    a, b = both(op, xa, Wt, y=torch.empty(M, N, device=dev, dtype=BF))
+    assert torch.equal(a["y"], b["y"])
+    want = O.gemv(xa.cpu(), W.cpu(), O.EPI_BF16)
+    assert_bf16_close(a["y"].cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
+    # gu: NORM + SWIGLU
+    N, Kd = SHAPES["gu"]
+    W = _weights(dev, N, Kd, 63, rows=2 * N)
+    Wt = gemv.tile_weights(W, swiglu=True)
+    op = gemv.Gemv(M, N, Kd, gemv.EPI_SWIGLU, norm=True)
+    assert cfg in op.candidates()
+    a, b = both(op, x, Wt, y=torch.empty(M, N, device=dev, dtype=BF), nw=nw)
+    assert torch.equal(a["y"], b["y"])
+    want = O.gemv(x.cpu(), W.cpu(), O.EPI_SWIGLU, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+    # 4 ulp: where the fp32 gate sum lies on a bf16 rounding tie, bf16(g) may round
+    # either way; one ulp of g moves silu(g) by silu'(g) / silu(g) x ulp(g), about
+    # 0.9 % at g = 0.52, 3 ulp of the product (seen at M = 40: g = 0.517578 in fp64)
+    assert_bf16_close(a["y"].cpu(), want, max_ulp=4, max_frac=0.03, atol=one_ulp_at(want))
+    # down (K = 9728) has no two-tile build
+    assert cfg not in gemv.Gemv(M, *SHAPES["down"], gemv.EPI_BF16, norm=False).candidates()
+
+
 @pytest.mark.parametrize("M", [2, 7, 16, 20])
 def test_gemv_split_k_layout(dev, M):
     """Layout 3 (MFMA tiles, K cut into slices merged by the last workgroup of
@@ -310,7 +380,8 @@ def test_gemv_stream_k_shapes(dev, M, N, Kd):
 
 @pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (3, (0, 8, 0)),
                                    (4, (0, 4, 0)), (16, (0, 8, 0)),
-                                   (3, (2, 1, 0)), (16, (2, 2, 0))])
+                                   (3, (2, 1, 0)), (16, (2, 2, 0)),
+                                   (20, (2, 1, 2)), (32, (2, 2, 2))])
 def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
     _, gemv = K()
     V, H = 151936, 2560
@@ -356,14 +427,15 @@ def test_lm_head_argmax_and_graph_replay(dev, M, cfg):
 
 
 @pytest.mark.parametrize("M,cfg", [(1, (0, 8, 0)), (2, (1, 2, 4)), (4, (0, 4, 0)),
-                                   (16, (2, 1, 0)), (20, (0, 8, 0))])
+                                   (16, (2, 1, 0)), (20, (0, 8, 0)), (40, (2, 1, 2))])
 def test_lm_head_step_tail(dev, M, cfg):
     """ko_lm_head_argmax: the LM head with the decode step's tail. The ids, logits,
     position advance and embedding gather equal ko_gemv's ARGMAX epilogue; the
     RoPE rows of the advanced positions equal rope_rows (and the table rows, the
     last position clamped to the table); the ids land in the pinned host ring at
     row ring_ctr[m], which advances and wraps, on eager calls and graph replays
-    (M = 20 runs as two launch slices of 16 and 4 rows)."""
+    (M = 20 runs as two launch slices of 16 and 4 rows, M = 40 on two row tiles
+    as slices of 32 and 8)."""
     fused, gemv = K()
     V, H, d, rows = 151936, 2560, 128, 40
     g = _g(dev, 50)
