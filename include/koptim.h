@@ -243,8 +243,10 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           workgroup, so every workgroup streams the same bytes; the last of
  *           a tile's workgroups adds their fp32 partial tiles in workgroup
  *           order (deterministic) and runs the epilogue. F32, BF16 or RESID, no
- *           NORM. part is its scratch (part_len >= ko_gemv_argmax_scratch(N, 4,
- *           10, 0)), with the rules of layout 3's.
+ *           NORM. `waves` 0, or 2 for two row tiles (M <= 32 per launch slice,
+ *           x of both tiles loaded per K step with the weights). part is its
+ *           scratch (part_len >= ko_gemv_argmax_scratch(N, 4, 10, waves)), with
+ *           the rules of layout 3's.
  * K % 8 == 0. M larger than a slice is processed in several launches. */
 int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* ss, void* h,
             float* ss_out, long long* ids, int* pos_inc, const void* next_emb, void* next_h,

@@ -27,7 +27,8 @@ int launch_layout2(const GemvArgs& a, int epi, bool norm, int per_cu, int mt, hi
 int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, float* slots,
                    hipStream_t s);
 // layout 4: MFMA tiles cut into SK_CPT chunks dealt out SK_W per workgroup
-int launch_layout4(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s);
+// layout 4: stream-K over the tiles' K chunks; mt row tiles of 16 rows of x per weight pass
+int launch_layout4(const GemvArgs& a, int epi, int mt, int* ctr, float* slots, hipStream_t s);
 
 // Workgroups of the layout-2 grid: at most MFMA_CUS * per_cu, and of those the
 // fewest that keep the most tiles per workgroup at its minimum, so every
@@ -52,10 +53,10 @@ inline bool mfma_supported(int K, int epi, int mt = 1) {
   return K == 2560 || K == 4096 || (K == 9728 && epi != EPI_SWIGLU);
 }
 
-// Rows of x per launch of a layout: 4 (layout 1), 32 (layout 2 with two row
-// tiles, waves == 2), else 16.
+// Rows of x per launch of a layout: 4 (layout 1), 32 (layouts 2 and 4 with two
+// row tiles, waves == 2), else 16.
 inline int mstep_for(int layout, int waves) {
-  return layout == 1 ? 4 : (layout == 2 && waves == 2) ? 32 : 16;
+  return layout == 1 ? 4 : ((layout == 2 || layout == 4) && waves == 2) ? 32 : 16;
 }
 
 // Steps per wavefront of layout 3 for K and a slice count (0: unsupported):
@@ -83,9 +84,11 @@ inline int sk_steps(int K) {
   return (S == 19 || S == 8 || S == 5) ? S : 0;
 }
 inline int sk_grid(int N) { return ((N + 15) / 16 * SK_CPT + SK_W - 1) / SK_W; }
-inline long long sk_scratch(int N) {
+// layout 4's scratch: the tiles' arrival counters (padded to 64), then each
+// tile's SK_SPT slots of mt * 256 floats (mt row tiles of 16 x 16)
+inline long long sk_scratch(int N, int mt = 1) {
   const long long T = (N + 15) / 16;
-  return ((T + 63) / 64) * 64 + T * SK_SPT * 256;
+  return ((T + 63) / 64) * 64 + T * SK_SPT * 256 * mt;
 }
 
 }  // namespace ko

@@ -400,12 +400,18 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
 // counter. The last of a tile's (2 or 3) workgroups adds the slots in
 // workgroup order (the result does not depend on the arrival order), re-arms
 // the counter and runs the epilogue.
-template <int EPI, int S, int PD>
+// MT = 2: 32 rows of x, two MFMAs per weight load. x of both row tiles is
+// loaded per K step with the weights (from L2: every tile reads all of x)
+// instead of being held for the chunk (19 steps x 2 tiles would take 152
+// VGPRs); rows past mrows load row 0 and are zeroed at the MFMA. Each merge
+// thread handles rows m and m + 16 of its column.
+template <int EPI, int S, int PD, int MT = 1>
 __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int* __restrict__ ctr,
                                                                 float* __restrict__ slots) {
   static_assert(EPI != EPI_ARGMAX && EPI != EPI_SWIGLU, "layout 4: F32, BF16 or RESID");
   static_assert(PD <= S, "the weight ring holds at most the chunk");
-  __shared__ float s_c[SK_W][16][17];
+  static_assert(MT == 1 || MT == 2, "16 or 32 rows of x");
+  __shared__ float s_c[SK_W][16 * MT][17];
   __shared__ int s_prev[2];
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, mr = a.mrows;
@@ -418,22 +424,31 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   const int sb = (cl - tile * SK_CPT) * S;        // its first K step
   const int kw0 = sb * 32 + 8 * g;
   const bool mok = col < mr;
+  const bool mok2 = col + 16 < mr;                // MT = 2: row col + 16 exists
 
   const uint16_t* wlane = a.w + 8 * lane;
+  const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+  const uint16_t* xrow2 = a.x + (long long)(mok2 ? col + 16 : 0) * K + kw0;
   uint4 wb[PD];
+  uint4 xb[MT > 1 ? PD : 1][2];  // MT = 2: the step's x of both row tiles
   auto issue = [&](int st, int slot) {
+    if constexpr (MT > 1) {
+      xb[slot][0] = ldg16(xrow + 32 * st);
+      xb[slot][1] = ldg16(xrow2 + 32 * st);
+    }
     wb[slot] = ldg16_stream(wlane + ((long long)tile * KS + sb + st) * 512);
   };
-  // RESID: the residual element this thread writes if its thread group's tile
+  // RESID: the residual elements this thread writes if its thread group's tile
   // (t0 + t / 256) is merged here, loaded with x
-  uint16_t hpre = 0;
+  uint16_t hpre[MT] = {};
   if constexpr (EPI == EPI_RESID) {
     const int tp = c0 / SK_CPT + (t >> 8);
-    hpre = resid_load(a, (t >> 4) & 15, (tp < T ? tp : T - 1) * 16 + (t & 15));
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+      hpre[u] = resid_load(a, 16 * u + ((t >> 4) & 15), (tp < T ? tp : T - 1) * 16 + (t & 15));
   }
-  bf16x8 xa[S];
-  {
-    const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
+  bf16x8 xa[MT == 1 ? S : 1];
+  if constexpr (MT == 1) {
     uint4 xr[S];
 #pragma unroll
     for (int st = 0; st < S; ++st) xr[st] = mok ? ldg16(xrow + 32 * st) : make_uint4(0, 0, 0, 0);
@@ -443,18 +458,39 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
     __builtin_amdgcn_sched_barrier(0);  // the whole ring issued here
 #pragma unroll
     for (int st = 0; st < S; ++st) xa[st] = __builtin_bit_cast(bf16x8, xr[st]);
+  } else {
+#pragma unroll
+    for (int st = 0; st < PD; ++st) issue(st, st);
+    __builtin_amdgcn_sched_barrier(0);  // the whole ring issued here
   }
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < S; ++st) {
     const int slot = st % PD;
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], __builtin_bit_cast(bf16x8, wb[slot]), acc,
-                                                  0, 0, 0);
+    if constexpr (MT == 1) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], __builtin_bit_cast(bf16x8, wb[slot]),
+                                                    acc, 0, 0, 0);
+    } else {
+      // zero the rows past mrows with masks (a select between the ring entry and
+      // a zero vector would be turned into a select of addresses, in scratch)
+      const uint32_t k1 = mok ? ~0u : 0u, k2 = mok2 ? ~0u : 0u;
+      const uint4 v1 = xb[slot][0], v2 = xb[slot][1];
+      const uint4 x1 = make_uint4(v1.x & k1, v1.y & k1, v1.z & k1, v1.w & k1);
+      const uint4 x2 = make_uint4(v2.x & k2, v2.y & k2, v2.z & k2, v2.w & k2);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1),
+                                                    __builtin_bit_cast(bf16x8, wb[slot]), acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x2),
+                                                     __builtin_bit_cast(bf16x8, wb[slot]), acc2, 0, 0, 0);
+    }
     if (st + PD < S) issue(st + PD, slot);
   }
-  // C lane layout: column col, rows 4g + i.
+  // C lane layout: column col, rows 4g + i (16 + 4g + i for the second row tile).
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_c[wv][4 * g + i][col] = acc[i];
+  if constexpr (MT > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_c[wv][16 + 4 * g + i][col] = acc2[i];
+  }
   __syncthreads();
 
   const int clast = (c0 + SK_W < nch ? c0 + SK_W : nch) - 1;
@@ -463,20 +499,27 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   const int tt = t0 + gi;
   const bool grp = gi <= t1 - t0;                   // uniform per wavefront
   const int r = t & 255, m = r >> 4, j = r & 15, n = tt * 16 + j;
-  float tot = 0.f;
+  float tot[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) tot[u] = 0.f;
   int nwg = 1, sl = 0;
   if (grp) {
     const int v0 = (tt * SK_CPT > c0 ? tt * SK_CPT : c0) - c0;
     const int v1 = ((tt + 1) * SK_CPT < clast + 1 ? (tt + 1) * SK_CPT : clast + 1) - c0;
-    for (int v = v0; v < v1; ++v) tot += s_c[v][m][j];
+    for (int v = v0; v < v1; ++v)
+#pragma unroll
+      for (int u = 0; u < MT; ++u) tot[u] += s_c[v][16 * u + m][j];
     const int first = tt * SK_CPT / SK_W;
     nwg = (tt * SK_CPT + SK_CPT - 1) / SK_W - first + 1;
     sl = blockIdx.x - first;
-    if (nwg > 1)
-      __hip_atomic_store(slots + ((long long)tt * SK_SPT + sl) * 256 + r, tot, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (nwg > 1) {
+#pragma unroll
+      for (int u = 0; u < MT; ++u)
+        __hip_atomic_store(slots + (((long long)tt * SK_SPT + sl) * MT + u) * 256 + r, tot[u],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's slot store is performed
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's slot stores are performed
   __syncthreads();
   if (grp && r == 0 && nwg > 1)
     s_prev[gi] = __hip_atomic_fetch_add(ctr + tt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -484,25 +527,35 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   if (!grp) return;
   if (nwg > 1) {
     if (s_prev[gi] != nwg - 1) return;
-    const float* base = slots + (long long)tt * SK_SPT * 256 + r;
-    float v[SK_SPT];
+    const float* base = slots + (long long)tt * SK_SPT * MT * 256 + r;
+    float v[SK_SPT][MT];
 #pragma unroll
     for (int q = 0; q < SK_SPT; ++q)
-      v[q] = q < nwg ? __hip_atomic_load(base + q * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                     : 0.f;
-    tot = 0.f;
 #pragma unroll
-    for (int q = 0; q < SK_SPT; ++q)
-      if (q < nwg) tot += v[q];
+      for (int u = 0; u < MT; ++u)
+        v[q][u] = q < nwg ? __hip_atomic_load(base + (q * MT + u) * 256, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : 0.f;
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      tot[u] = 0.f;
+#pragma unroll
+      for (int q = 0; q < SK_SPT; ++q)
+        if (q < nwg) tot[u] += v[q][u];
+    }
     if (r == 0) __hip_atomic_store(ctr + tt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  const bool ok = m < mr && n < N;
-  float h2 = 0.f;
-  if (ok) h2 = epilogue<EPI>(a, m, n, tot, 0.f, &hpre);
-  if constexpr (EPI == EPI_RESID) {
-    if (a.ss_out) {
-      h2 = row_sum16(h2);
-      if (j == 0 && m < mr) atomicAdd(a.ss_out + m, h2);
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const int mm = 16 * u + m;
+    const bool ok = mm < mr && n < N;
+    float h2 = 0.f;
+    if (ok) h2 = epilogue<EPI>(a, mm, n, tot[u], 0.f, &hpre[u]);
+    if constexpr (EPI == EPI_RESID) {
+      if (a.ss_out) {
+        h2 = row_sum16(h2);
+        if (j == 0 && mm < mr) atomicAdd(a.ss_out + mm, h2);
+      }
     }
   }
 }
@@ -615,24 +668,29 @@ int launch_mfma_ks(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, 
 }
 
 
-template <int S, int PD>
+template <int S, int PD, int MT = 1>
 int launch_mfma_sk_s(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
   const dim3 grid(sk_grid(a.N));
+#define KO_S(EPIV) \
+  hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPIV, S, PD, MT>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots)
   switch (epi) {
-    case EPI_F32:
-      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_F32, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
-      break;
-    case EPI_BF16:
-      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_BF16, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
-      break;
-    default:
-      hipLaunchKernelGGL((gemv_mfma_sk_kernel<EPI_RESID, S, PD>), grid, dim3(64 * SK_W), 0, s, a, ctr, slots);
-      break;
+    case EPI_F32: KO_S(EPI_F32); break;
+    case EPI_BF16: KO_S(EPI_BF16); break;
+    default: KO_S(EPI_RESID); break;
   }
+#undef KO_S
   return KO_LAUNCH_STATUS();
 }
 
-int launch_mfma_sk(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
+int launch_mfma_sk(const GemvArgs& a, int epi, int mt, int* ctr, float* slots, hipStream_t s) {
+  if (mt == 2) {  // 32 rows: x of both row tiles loaded per K step
+    switch (sk_steps(a.K)) {
+      case 19: return launch_mfma_sk_s<19, 8, 2>(a, epi, ctr, slots, s);
+      case 8: return launch_mfma_sk_s<8, 8, 2>(a, epi, ctr, slots, s);
+      case 5: return launch_mfma_sk_s<5, 5, 2>(a, epi, ctr, slots, s);
+      default: return KO_ENOTSUP;
+    }
+  }
   switch (sk_steps(a.K)) {
     case 19: return launch_mfma_sk_s<19, 10>(a, epi, ctr, slots, s);
     case 8: return launch_mfma_sk_s<8, 8>(a, epi, ctr, slots, s);
@@ -655,8 +713,8 @@ int launch_layout3(const GemvArgs& a, int epi, bool norm, int slices, int* ctr, 
   return launch_mfma_ks(a, epi, norm, slices, ctr, slots, s);
 }
 
-int launch_layout4(const GemvArgs& a, int epi, int* ctr, float* slots, hipStream_t s) {
-  return launch_mfma_sk(a, epi, ctr, slots, s);
+int launch_layout4(const GemvArgs& a, int epi, int mt, int* ctr, float* slots, hipStream_t s) {
+  return launch_mfma_sk(a, epi, mt, ctr, slots, s);
 }
 
 }  // namespace ko

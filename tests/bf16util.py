@@ -35,3 +35,21 @@ def assert_bf16_close(got, want, max_ulp=1, max_frac=0.01, atol=0.0):
 def one_ulp_at(t):
     """Absolute size of one bf16 ulp at the tensor's typical magnitude."""
     return 2.0 ** -7 * rms(t)
+
+
+def bf16_ulp(t):
+    """One bf16 ulp at each element's own magnitude (2^(floor(log2|v|) - 7));
+    the smallest normal's ulp at zero."""
+    _, e = torch.frexp(t.float().abs().clamp_min(2.0 ** -126))
+    return torch.ldexp(torch.ones_like(t, dtype=torch.float32), e - 8)
+
+
+def assert_resid_close(got, want, y, max_frac=0.02):
+    """h <- bf16(h + bf16(y)) against the oracle's: the fp32 sums y may round to
+    bf16 one ulp of y apart (near a tie), which the second rounding carries into
+    h as up to ulp(y) + ulp(h) (many ulps of h where h + y cancels)."""
+    d = (got.float() - want.float()).abs()
+    bound = bf16_ulp(y) + bf16_ulp(want)
+    bad = d > bound
+    assert not bool(bad.any()), f"{int(bad.sum())} elements beyond ulp(y) + ulp(h)"
+    assert float((d > 0).float().mean()) <= max_frac, f"mismatch fraction {float((d > 0).float().mean())}"

@@ -114,6 +114,18 @@ def test_gemv_host_path_of_every_layout_without_gpu(libpath):
         st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 20, 2560, K,
                        epi, 0, 0, 2, 1, waves, 1e-6, None)
         assert st == -95, (K, epi, waves, st)
+    # layout 4 with two row tiles: scratch slots of 32 x 16 floats
+    for M, K in [(20, 9728), (40, 4096), (32, 2560)]:
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, M, 2560, K,
+                       1, 0, 0, 4, 10, 2, 1e-6, None)
+        assert st > 0, (M, K, st)
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 20, 2560, 9728,
+                   1, 0, 0, 4, 10, 1, 1e-6, None)
+    assert st == -95
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P,
+                   192 + 160 * 3 * 256, 20, 2560, 9728, 1, 0, 0, 4, 10, 2, 1e-6, None)
+    assert st == -34   # the one-tile scratch is too small for two tiles
+    assert h.ko_gemv_argmax_scratch(2560, 4, 10, 2) == 192 + 160 * 3 * 512
     # ARGMAX partials: 160 tiles on 160 workgroups, 16 or 32 rows each
     assert h.ko_gemv_argmax_scratch(2560, 2, 1, 0) == 2 * 16 * 160
     assert h.ko_gemv_argmax_scratch(2560, 2, 1, 2) == 2 * 32 * 160

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import ops as O
-from tests.bf16util import assert_bf16_close, one_ulp_at
+from tests.bf16util import assert_bf16_close, assert_resid_close, one_ulp_at
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -228,7 +228,7 @@ def test_gemv_two_row_tiles(dev, M, cfg):
     assert cfg in op.candidates()
     a, b = both(op, xa, Wt, h=h, ss_out=torch.full((M,), 5.0, device=dev))
     assert torch.equal(a["h"], b["h"])
-    assert_bf16_close(a["h"].cpu(), hr, max_frac=0.02, atol=one_ulp_at(hr))
+    assert_resid_close(a["h"].cpu(), hr, O.gemv(xa.cpu(), W.cpu(), O.EPI_F32))
     torch.testing.assert_close(a["ss_out"].cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
     op = gemv.Gemv(M, N, Kd, gemv.EPI_BF16, norm=False)
     a, b = both(op, xa, Wt, y=torch.empty(M, N, device=dev, dtype=BF))
@@ -250,6 +250,48 @@ def test_gemv_two_row_tiles(dev, M, cfg):
     assert_bf16_close(a["y"].cpu(), want, max_ulp=4, max_frac=0.03, atol=one_ulp_at(want))
     # down (K = 9728) has no two-tile build
     assert cfg not in gemv.Gemv(M, *SHAPES["down"], gemv.EPI_BF16, norm=False).candidates()
+
+
+@pytest.mark.parametrize("M", [17, 32, 40])
+def test_gemv_stream_k_two_row_tiles(dev, M):
+    """Layout 4 with two row tiles (x of rows 0-15 and 16-31 loaded per K step
+    with the weights) at every K it takes (2560, 4096, 9728): each row equals the
+    one-tile launch bit for bit and the oracle within the bf16 tolerance."""
+    _, gemv = K()
+    g = _g(dev, 70 + M)
+    cases = [("o", gemv.EPI_RESID), ("o", gemv.EPI_BF16), ("down", gemv.EPI_BF16),
+             ("down", gemv.EPI_F32), ("down", gemv.EPI_RESID), ("qkv", gemv.EPI_BF16)]
+    for shape, epi in cases:
+        N, Kd = SHAPES[shape]
+        x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+        W = _weights(dev, N, Kd, 71)
+        Wt = gemv.tile_weights(W)
+        op = gemv.Gemv(M, N, Kd, epi, norm=False)
+        assert (4, 10, 2) in op.candidates()
+        outs = []
+        h0 = torch.randn(M, N, device=dev, generator=g).to(BF)
+        for cfg in ((4, 10, 2), (4, 10, 0)):
+            if epi == gemv.EPI_RESID:
+                h, ss_out = h0.clone(), torch.full((M,), 5.0, device=dev)
+                op(x, Wt, h=h, ss_out=ss_out, cfg=cfg)
+                outs.append((h, ss_out))
+            else:
+                y = torch.empty(M, N, device=dev, dtype=torch.float32 if epi == gemv.EPI_F32 else BF)
+                op(x, Wt, y=y, cfg=cfg)
+                outs.append((y,))
+            torch.cuda.synchronize()
+        assert torch.equal(outs[0][0], outs[1][0]), (shape, epi)
+        if epi == gemv.EPI_RESID:
+            want, ssr = O.gemv(x.cpu(), W.cpu(), O.EPI_RESID, h=h0.cpu())
+            y = O.gemv(x.cpu(), W.cpu(), O.EPI_F32)
+            assert_resid_close(outs[0][0].cpu(), want, y)
+            torch.testing.assert_close(outs[0][1].cpu(), ssr + 5.0, rtol=1e-3, atol=1e-2)
+        elif epi == gemv.EPI_BF16:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_BF16)
+            assert_bf16_close(outs[0][0].cpu(), want, max_frac=0.02, atol=one_ulp_at(want))
+        else:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32)
+            torch.testing.assert_close(outs[0][0].cpu(), want, rtol=2e-3, atol=2e-3)
 
 
 @pytest.mark.parametrize("M", [2, 7, 16, 20])
