@@ -685,7 +685,7 @@ int launch_mfma_sk_s(const GemvArgs& a, int epi, int* ctr, float* slots, hipStre
 int launch_mfma_sk(const GemvArgs& a, int epi, int mt, int* ctr, float* slots, hipStream_t s) {
   if (mt == 2) {  // 32 rows: x of both row tiles loaded per K step
     switch (sk_steps(a.K)) {
-      case 19: return launch_mfma_sk_s<19, 8, 2>(a, epi, ctr, slots, s);
+      case 19: return launch_mfma_sk_s<19, 12, 2>(a, epi, ctr, slots, s);
       case 8: return launch_mfma_sk_s<8, 8, 2>(a, epi, ctr, slots, s);
       case 5: return launch_mfma_sk_s<5, 5, 2>(a, epi, ctr, slots, s);
       default: return KO_ENOTSUP;
