@@ -192,6 +192,30 @@ def test_hipblaslt_decode_graph_qwen3_4b_width(dev):
     assert err < LOGIT_ATOL
 
 
+@pytest.mark.parametrize("B", [32, 40])
+def test_fused_decode_graph_above_16_rows(dev, B):
+    """The fused decode graph, forced, at 32 and 40 sequences (2-layer Qwen3-4B
+    width): the GEMVs run 32-row slices (two MFMA row tiles per weight pass, where
+    the tuner takes them) and, at 40, an 8-row slice after them. Tokens and
+    logits against the oracle's teacher-forced replay, as the B = 3 hipBLASLt
+    test."""
+    cfg = Qwen3Config(layers=2)
+    w = random_weights(cfg, seed=9)
+    prompt = torch.randint(0, cfg.vocab, (B, 48), generator=torch.Generator().manual_seed(B))
+    n = 8
+    eng = _engine(cfg, w, decode_graph="fused")
+    toks, logits = eng.trace(prompt.tolist(), n)
+    assert eng.step_kind == "fused"
+    cfgs = {k: g.cfg for k, g in eng.gv.items()}
+    del eng
+    torch.cuda.empty_cache()
+    replay = Qwen3Oracle(cfg, w, B=B, cap=64).teacher_forced(prompt, toks)
+    agree, err = check_against_replay(toks, logits, replay)
+    print(f"fused graph B={B}, 2-layer Qwen3-4B width: GEMV configs {cfgs}, agreement "
+          f"{agree:.3f}, max |dlogit| {err:.4f}")
+    assert err < LOGIT_ATOL
+
+
 def test_auto_keeps_the_faster_decode_graph(dev):
     cfg = SMALL
     w = perturbed_weights(cfg, seed=11)
