@@ -243,8 +243,9 @@ int ko_embed_ss(const long long* ids, const void* emb, void* h, float* ss, int M
  *           workgroup, so every workgroup streams the same bytes; the last of
  *           a tile's workgroups adds their fp32 partial tiles in workgroup
  *           order (deterministic) and runs the epilogue. F32, BF16 or RESID, no
- *           NORM. `waves` 0, or 2 for two row tiles (M <= 32 per launch slice,
- *           x of both tiles loaded per K step with the weights). part is its
+ *           NORM. `waves` 0, or 2 / 4 for two / four row tiles (M <= 32 / 64
+ *           per launch slice, x of every tile loaded per K step with the
+ *           weights; a slice runs on the fewest tiles that hold it). part is its
  *           scratch (part_len >= ko_gemv_argmax_scratch(N, 4, 10, waves)), with
  *           the rules of layout 3's.
  * K % 8 == 0. M larger than a slice is processed in several launches. */

@@ -297,8 +297,8 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
   } else if (layout == 4) {
     if (norm || epi == EPI_ARGMAX || epi == EPI_SWIGLU || rows != SK_W || !sk_steps(K))
       return KO_ENOTSUP;
-    if (waves != 0 && waves != 2) return KO_ENOTSUP;  // row tiles: 0 (one) or 2
-    if (!part || !al16(part) || part_len < sk_scratch(N, waves == 2 ? 2 : 1)) return KO_ERANGE;
+    if (waves != 0 && waves != 2 && waves != 4) return KO_ENOTSUP;  // row tiles: 0 (one), 2, 4
+    if (!part || !al16(part) || part_len < sk_scratch(N, waves ? waves : 1)) return KO_ERANGE;
   } else {
     return KO_EINVAL;
   }
@@ -342,7 +342,7 @@ int gemv_impl(const void* x, const void* w, void* y, const void* nw, const float
       st = launch_layout3(a, epi, norm != 0, rows, reinterpret_cast<int*>(part),
                           part + ((N + 15) / 16 + 63) / 64 * 64, s);
     else
-      st = launch_layout4(a, epi, waves == 2 && mr > 16 ? 2 : 1, reinterpret_cast<int*>(part),
+      st = launch_layout4(a, epi, sk_tiles(waves, mr), reinterpret_cast<int*>(part),
                           part + ((N + 15) / 16 + 63) / 64 * 64, s);
     if (st) return st;
     if (epi == EPI_ARGMAX) {
@@ -430,7 +430,7 @@ int ko_argmax_rows(const void* x, long long ld, int M, int N, long long* ids, vo
 long long ko_gemv_argmax_scratch(int N, int layout, int rows, int waves) {
   if (N < 1 || rows < 1 || (layout == 1 && waves < 1) || layout < 0 || layout > 4) return -1;
   if (layout == 3) return rows > 1 ? ks_scratch(N, rows) : 0;
-  if (layout == 4) return sk_scratch(N, waves == 2 ? 2 : 1);
+  if (layout == 4) return sk_scratch(N, waves == 2 || waves == 4 ? waves : 1);
   return 2LL * mstep_for(layout, waves) * parts_for(N, layout, rows, waves);
 }
 

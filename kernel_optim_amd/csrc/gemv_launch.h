@@ -54,9 +54,18 @@ inline bool mfma_supported(int K, int epi, int mt = 1) {
 }
 
 // Rows of x per launch of a layout: 4 (layout 1), 32 (layouts 2 and 4 with two
-// row tiles, waves == 2), else 16.
+// row tiles, waves == 2), 64 (layout 4 with four, waves == 4), else 16.
 inline int mstep_for(int layout, int waves) {
-  return layout == 1 ? 4 : ((layout == 2 || layout == 4) && waves == 2) ? 32 : 16;
+  if (layout == 1) return 4;
+  if ((layout == 2 || layout == 4) && waves == 2) return 32;
+  if (layout == 4 && waves == 4) return 64;
+  return 16;
+}
+// Row tiles of a launch slice of mr rows under a layout-4 `waves` (0, 2 or 4):
+// the fewest that hold the slice.
+inline int sk_tiles(int waves, int mr) {
+  if (waves == 0) return 1;
+  return mr > 32 && waves == 4 ? 4 : mr > 16 ? 2 : 1;
 }
 
 // Steps per wavefront of layout 3 for K and a slice count (0: unsupported):

@@ -404,13 +404,13 @@ __global__ __launch_bounds__(64 * KSW) void gemv_mfma_ks_kernel(GemvArgs a, int*
 // loaded per K step with the weights (from L2: every tile reads all of x)
 // instead of being held for the chunk (19 steps x 2 tiles would take 152
 // VGPRs); rows past mrows load row 0 and are zeroed at the MFMA. Each merge
-// thread handles rows m and m + 16 of its column.
+// thread handles rows m, m + 16, ... of its column. MT = 4: 64 rows the same way.
 template <int EPI, int S, int PD, int MT = 1>
 __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int* __restrict__ ctr,
                                                                 float* __restrict__ slots) {
   static_assert(EPI != EPI_ARGMAX && EPI != EPI_SWIGLU, "layout 4: F32, BF16 or RESID");
   static_assert(PD <= S, "the weight ring holds at most the chunk");
-  static_assert(MT == 1 || MT == 2, "16 or 32 rows of x");
+  static_assert(MT == 1 || MT == 2 || MT == 4, "16, 32 or 64 rows of x");
   __shared__ float s_c[SK_W][16 * MT][17];
   __shared__ int s_prev[2];
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63, col = lane & 15, g = lane >> 4;
@@ -424,17 +424,24 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
   const int sb = (cl - tile * SK_CPT) * S;        // its first K step
   const int kw0 = sb * 32 + 8 * g;
   const bool mok = col < mr;
-  const bool mok2 = col + 16 < mr;                // MT = 2: row col + 16 exists
 
   const uint16_t* wlane = a.w + 8 * lane;
   const uint16_t* xrow = a.x + (long long)(mok ? col : 0) * K + kw0;
-  const uint16_t* xrow2 = a.x + (long long)(mok2 ? col + 16 : 0) * K + kw0;
+  // MT > 1: row col + 16 u of row tile u (row 0 when past mrows, then masked)
+  const uint16_t* xrows[MT];
+  uint32_t xmask[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const bool ok = col + 16 * u < mr;
+    xrows[u] = a.x + (long long)(ok ? col + 16 * u : 0) * K + kw0;
+    xmask[u] = ok ? ~0u : 0u;
+  }
   uint4 wb[PD];
-  uint4 xb[MT > 1 ? PD : 1][2];  // MT = 2: the step's x of both row tiles
+  uint4 xb[MT > 1 ? PD : 1][MT];  // MT > 1: the step's x of every row tile
   auto issue = [&](int st, int slot) {
     if constexpr (MT > 1) {
-      xb[slot][0] = ldg16(xrow + 32 * st);
-      xb[slot][1] = ldg16(xrow2 + 32 * st);
+#pragma unroll
+      for (int u = 0; u < MT; ++u) xb[slot][u] = ldg16(xrows[u] + 32 * st);
     }
     wb[slot] = ldg16_stream(wlane + ((long long)tile * KS + sb + st) * 512);
   };
@@ -463,34 +470,35 @@ __global__ __launch_bounds__(64 * SK_W) void gemv_mfma_sk_kernel(GemvArgs a, int
     for (int st = 0; st < PD; ++st) issue(st, st);
     __builtin_amdgcn_sched_barrier(0);  // the whole ring issued here
   }
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) acc[u] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < S; ++st) {
     const int slot = st % PD;
     if constexpr (MT == 1) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], __builtin_bit_cast(bf16x8, wb[slot]),
-                                                    acc, 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], __builtin_bit_cast(bf16x8, wb[slot]),
+                                                       acc[0], 0, 0, 0);
     } else {
       // zero the rows past mrows with masks (a select between the ring entry and
       // a zero vector would be turned into a select of addresses, in scratch)
-      const uint32_t k1 = mok ? ~0u : 0u, k2 = mok2 ? ~0u : 0u;
-      const uint4 v1 = xb[slot][0], v2 = xb[slot][1];
-      const uint4 x1 = make_uint4(v1.x & k1, v1.y & k1, v1.z & k1, v1.w & k1);
-      const uint4 x2 = make_uint4(v2.x & k2, v2.y & k2, v2.z & k2, v2.w & k2);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1),
-                                                    __builtin_bit_cast(bf16x8, wb[slot]), acc, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x2),
-                                                     __builtin_bit_cast(bf16x8, wb[slot]), acc2, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < MT; ++u) {
+        const uint4 v = xb[slot][u];
+        const uint32_t k = xmask[u];
+        const uint4 xv = make_uint4(v.x & k, v.y & k, v.z & k, v.w & k);
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv),
+                                                         __builtin_bit_cast(bf16x8, wb[slot]),
+                                                         acc[u], 0, 0, 0);
+      }
     }
     if (st + PD < S) issue(st + PD, slot);
   }
-  // C lane layout: column col, rows 4g + i (16 + 4g + i for the second row tile).
+  // C lane layout: column col, rows 4g + i (16 u + 4g + i for row tile u).
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s_c[wv][4 * g + i][col] = acc[i];
-  if constexpr (MT > 1) {
+  for (int u = 0; u < MT; ++u)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s_c[wv][16 + 4 * g + i][col] = acc2[i];
-  }
+    for (int i = 0; i < 4; ++i) s_c[wv][16 * u + 4 * g + i][col] = acc[u][i];
   __syncthreads();
 
   const int clast = (c0 + SK_W < nch ? c0 + SK_W : nch) - 1;
@@ -683,6 +691,14 @@ int launch_mfma_sk_s(const GemvArgs& a, int epi, int* ctr, float* slots, hipStre
 }
 
 int launch_mfma_sk(const GemvArgs& a, int epi, int mt, int* ctr, float* slots, hipStream_t s) {
+  if (mt == 4) {  // 64 rows: x of four row tiles loaded per K step
+    switch (sk_steps(a.K)) {
+      case 19: return launch_mfma_sk_s<19, 6, 4>(a, epi, ctr, slots, s);
+      case 8: return launch_mfma_sk_s<8, 6, 4>(a, epi, ctr, slots, s);
+      case 5: return launch_mfma_sk_s<5, 5, 4>(a, epi, ctr, slots, s);
+      default: return KO_ENOTSUP;
+    }
+  }
   if (mt == 2) {  // 32 rows: x of both row tiles loaded per K step
     switch (sk_steps(a.K)) {
       case 19: return launch_mfma_sk_s<19, 12, 2>(a, epi, ctr, slots, s);

@@ -21,7 +21,7 @@ Additions of this backend:
 wavefront ``rows`` columns with ``waves`` wavefronts per workgroup sharing the
 normalised input through LDS (M <= 4); layouts 2, 3 and 4 put 2..16 rows on
 MFMA tiles (layouts 2 and 4 with ``waves`` = 2: 32 rows, two row tiles sharing
-each weight load) and read a tiled copy of the weights (``tile_weights``), layout 3 with
+each weight load; layout 4 with ``waves`` = 4: 64 rows) and read a tiled copy of the weights (``tile_weights``), layout 3 with
 the K range of a tile cut into ``rows`` slices merged by the tile's last slice,
 layout 4 with each tile cut into 16 K chunks dealt out 10 per workgroup and
 merged by the tile's last workgroup (no atomics on the output in either, so the
@@ -111,14 +111,15 @@ class Gemv:
         of at most 256 x per_cu workgroups, the fewest that keep the most tiles
         per workgroup at its minimum; ``(2, per_cu, 2)``: 32 rows per weight
         pass, offered above 16 rows), layout 3 splits its tiles' K range and
-        layout 4 (``(4, 10, 0)``; ``(4, 10, 2)`` with 32 rows) deals the tiles'
-        16 K chunks out 10 per workgroup."""
+        layout 4 (``(4, 10, 0)``; ``(4, 10, 2)`` / ``(4, 10, 4)`` with 32 / 64
+        rows) deals the tiles' 16 K chunks out 10 per workgroup."""
         out = []
         mfma = [(2, 2, 0), (2, 1, 0)] if self.M >= 2 and self.mfma_ok() else []
         mfma += [(2, 2, 2), (2, 1, 2)] if self.M > 16 and self.mfma2_ok() else []
         mfma += [(3, s, 0) for s in self.ks_slices()] if self.M >= 2 else []
         mfma += [(4, 10, 0)] if self.M >= 2 and self.sk_ok() else []
         mfma += [(4, 10, 2)] if self.M > 16 and self.sk_ok() else []
+        mfma += [(4, 10, 4)] if self.M > 32 and self.sk_ok() else []
         if self.M <= 4 and (not self.norm or self.M * self.K * 2 <= 40960):
             per_wave = (4, 2, 1) if self.N >= 32768 else (1, 2, 4)
             for rows in per_wave:

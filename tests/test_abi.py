@@ -126,6 +126,18 @@ def test_gemv_host_path_of_every_layout_without_gpu(libpath):
                    192 + 160 * 3 * 256, 20, 2560, 9728, 1, 0, 0, 4, 10, 2, 1e-6, None)
     assert st == -34   # the one-tile scratch is too small for two tiles
     assert h.ko_gemv_argmax_scratch(2560, 4, 10, 2) == 192 + 160 * 3 * 512
+    # four row tiles: 64 rows per launch slice, slots of 64 x 16 floats
+    for M in (40, 64, 100):
+        st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, M, 2560,
+                       9728, 1, 0, 0, 4, 10, 4, 1e-6, None)
+        assert st > 0, (M, st)
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P,
+                   192 + 160 * 3 * 512, 40, 2560, 9728, 1, 0, 0, 4, 10, 4, 1e-6, None)
+    assert st == -34
+    assert h.ko_gemv_argmax_scratch(2560, 4, 10, 4) == 192 + 160 * 3 * 1024
+    st = h.ko_gemv(P, P, P, P, None, P, None, None, None, None, None, P, 1 << 30, 40, 2560, 9728,
+                   1, 0, 0, 4, 10, 3, 1e-6, None)
+    assert st == -95
     # ARGMAX partials: 160 tiles on 160 workgroups, 16 or 32 rows each
     assert h.ko_gemv_argmax_scratch(2560, 2, 1, 0) == 2 * 16 * 160
     assert h.ko_gemv_argmax_scratch(2560, 2, 1, 2) == 2 * 32 * 160

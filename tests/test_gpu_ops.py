@@ -252,13 +252,16 @@ def test_gemv_two_row_tiles(dev, M, cfg):
     assert cfg not in gemv.Gemv(M, *SHAPES["down"], gemv.EPI_BF16, norm=False).candidates()
 
 
-@pytest.mark.parametrize("M", [17, 32, 40])
-def test_gemv_stream_k_two_row_tiles(dev, M):
-    """Layout 4 with two row tiles (x of rows 0-15 and 16-31 loaded per K step
-    with the weights) at every K it takes (2560, 4096, 9728): each row equals the
-    one-tile launch bit for bit and the oracle within the bf16 tolerance."""
+@pytest.mark.parametrize("M,waves", [(17, 2), (32, 2), (40, 2), (40, 4), (64, 4), (70, 4)])
+def test_gemv_stream_k_two_row_tiles(dev, M, waves):
+    """Layout 4 with two or four row tiles (x of rows 0-15, 16-31, ... loaded per K
+    step with the weights) at every K it takes (2560, 4096, 9728): each row
+    equals the one-tile launch bit for bit and the oracle within the bf16
+    tolerance. M = 40 on four tiles leaves the last two part-filled; M = 70 runs
+    a 64-row slice and a 6-row slice on one tile."""
     _, gemv = K()
-    g = _g(dev, 70 + M)
+    cfg_mt = (4, 10, waves)
+    g = _g(dev, 70 + M + waves)
     cases = [("o", gemv.EPI_RESID), ("o", gemv.EPI_BF16), ("down", gemv.EPI_BF16),
              ("down", gemv.EPI_F32), ("down", gemv.EPI_RESID), ("qkv", gemv.EPI_BF16)]
     for shape, epi in cases:
@@ -267,10 +270,10 @@ def test_gemv_stream_k_two_row_tiles(dev, M):
         W = _weights(dev, N, Kd, 71)
         Wt = gemv.tile_weights(W)
         op = gemv.Gemv(M, N, Kd, epi, norm=False)
-        assert (4, 10, 2) in op.candidates()
+        assert cfg_mt in op.candidates()
         outs = []
         h0 = torch.randn(M, N, device=dev, generator=g).to(BF)
-        for cfg in ((4, 10, 2), (4, 10, 0)):
+        for cfg in (cfg_mt, (4, 10, 0)):
             if epi == gemv.EPI_RESID:
                 h, ss_out = h0.clone(), torch.full((M,), 5.0, device=dev)
                 op(x, Wt, h=h, ss_out=ss_out, cfg=cfg)
