@@ -339,7 +339,29 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
   if constexpr (Hooks::kNotify)
     if (total == 0 && wg == 0) hooks.no_units();
 
-  for (int u = wg; u < total; u += nwg) {
+  // 2..64 sequences with fixed units: the units are dealt out largest first, the
+  // full units (every sequence's first len / unit) and then the part-filled last
+  // units in decreasing size (ties: lower sequence first), in a snake order over
+  // the workgroups (forward on even rounds, backward on odd ones), so ragged
+  // lengths leave every workgroup about the same number of keys (with one
+  // round of units the order does not matter). Lane b holds sequence b's count
+  // of full units and its last unit's rank.
+  const bool balanced = small_b && a.B > 1 && a.usplit == 0 && total > nwg;
+  int my_f = 0, my_fincl = 0, my_rank = 0, my_rem = 0, nfull = 0;
+  if (balanced) {
+    my_f = my_len / unit;
+    my_rem = my_len - my_f * unit;
+    my_fincl = wave_incl_scan(my_f);
+    nfull = readlane(my_fincl, 63);
+    for (int j = 0; j < a.B; ++j) {
+      const int rj = readlane(my_rem, j);
+      my_rank += rj > my_rem || (rj == my_rem && j < lane) ? 1 : 0;
+    }
+  }
+
+  for (int k = 0;; ++k) {
+    const int u = k * nwg + (balanced && (k & 1) ? nwg - 1 - wg : wg);
+    if (u >= total) break;
     const bool pre = spec && u == wg;  // this unit's first loads are in flight already
     const int pidx = u / nkv;
     const int kvh = u - pidx * nkv;
@@ -348,6 +370,15 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
       b = 0;
       c = pidx;
       kv_len = len1;
+    } else if (balanced) {
+      if (pidx < nfull) {
+        b = uniform(__popcll(__ballot(my_fincl <= pidx)));
+        c = pidx - readlane(my_fincl - my_f, b);
+      } else {  // the part-filled unit of rank pidx - nfull
+        b = uniform(__builtin_ctzll(__ballot(my_rem > 0 && my_rank == pidx - nfull)));
+        c = readlane(my_f, b);
+      }
+      kv_len = readlane(my_len, b);
     } else if (small_b) {
       b = uniform(__popcll(__ballot(my_incl <= pidx)));
       c = pidx - readlane(my_incl - my_n, b);
