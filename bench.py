@@ -50,6 +50,9 @@ def parse_args():
                     help="skip the B=16 decode measurement (same workload at batch 16)")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the one-layer measurement (B=1, 4, 16 with 2048 cached keys)")
+    ap.add_argument("--decode-batches", default="",
+                    help="comma-separated further batch sizes of the same decode workload "
+                         "(e.g. 32,64), reported as decode_b<B>; not in the default run")
     ap.add_argument("--spec", action="store_true",
                     help="also measure B=1 decode with prompt-lookup speculation (the same "
                          "random prompt, and a prompt of a repeated 64-token pattern)")
@@ -534,6 +537,8 @@ def main():
         line["decode_b1"] = bench_decode(args, eng, B=1)
         if not args.no_decode_b16:
             line["decode_b16"] = bench_decode(args, eng, B=16)
+        for b in (int(x) for x in args.decode_batches.split(",") if x.strip()):
+            line[f"decode_b{b}"] = bench_decode(args, eng, B=b)
         del eng
         torch.cuda.empty_cache()
     if args.spec:
