@@ -30,7 +30,10 @@ extern "C" {
  *          Query t sits at position valid-T+t and sees keys < valid-T+t+1.
  * unit     keys per work unit (multiple of 16); max_units*unit >= cap. Each unit
  *          leaves one fp32 partial slot per query row.
- * grid_waves  number of wavefronts launched (they stride over the units). With
+ * grid_waves  number of wavefronts launched (they take the units in rounds; with
+ *          T == 1, 2-64 sequences and more than one round, the full units first and
+ *          the part-filled last units by decreasing size, forward and backward over
+ *          the workgroups in alternate rounds). With
  *          T == 1 a unit is split over the wavefronts of one workgroup: 4 when
  *          unit % 64 == 0, else 2 when unit % 32 == 0, else 1, so grid_waves
  *          should be a multiple of that count.
