@@ -423,6 +423,59 @@ def test_gemv_stream_k_shapes(dev, M, N, Kd):
             torch.testing.assert_close(outs[0].cpu(), want.float(), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("M,N,Kd,cfg", [(20, 200, 2560, (4, 10, 2)), (32, 1000, 4096, (4, 10, 2)),
+                                        (40, 2568, 9728, (4, 10, 2)), (40, 200, 2560, (4, 10, 4)),
+                                        (64, 1000, 4096, (4, 10, 4)), (50, 2568, 9728, (4, 10, 4)),
+                                        (20, 1000, 2560, (2, 1, 2)), (30, 200, 4096, (2, 2, 2))])
+def test_gemv_row_tiles_odd_shapes(dev, M, N, Kd, cfg):
+    """Two and four row tiles beyond the model's shapes: N not a multiple of 16 (a
+    part-filled last tile), few tiles (grids smaller than the CUs, layout-4 chunks
+    ending inside a workgroup), part-filled row tiles and 32/64-row slices followed
+    by a shorter one. Each output equals the one-tile launch bit for bit and the
+    oracle within the bf16 tolerance (F32, BF16, RESID; layout 2 also with the NORM
+    prologue, its row norms computed in the kernel)."""
+    _, gemv = K()
+    one = (cfg[0], cfg[1], 0)
+    g = _g(dev, 130 + M + N + cfg[2])
+    x = torch.randn(M, Kd, device=dev, generator=g).to(BF)
+    nw = (1 + 0.1 * torch.randn(Kd, device=dev, generator=g)).to(BF)
+    W = _weights(dev, N, Kd, 131 + N)
+    Wt = gemv.tile_weights(W)
+    cases = [(gemv.EPI_F32, False), (gemv.EPI_BF16, False), (gemv.EPI_RESID, False)]
+    if cfg[0] == 2:
+        cases.append((gemv.EPI_F32, True))
+    y_f32 = O.gemv(x.cpu(), W.cpu(), O.EPI_F32)
+    for epi, norm in cases:
+        op = gemv.Gemv(M, N, Kd, epi, norm=norm)
+        assert cfg in op.candidates(), (epi, norm)
+        kw = {"nw": nw} if norm else {}
+        h0 = torch.randn(M, N, device=dev, generator=_g(dev, 9)).to(BF)
+        outs = []
+        for c in (cfg, one):
+            if epi == gemv.EPI_RESID:
+                h = h0.clone()
+                op(x, Wt, h=h, cfg=c, **kw)
+                outs.append(h)
+            else:
+                y = torch.empty(M, N, device=dev, dtype=torch.float32 if epi == gemv.EPI_F32 else BF)
+                op(x, Wt, y=y, cfg=c, **kw)
+                outs.append(y)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), (epi, norm)
+        got = outs[0].cpu()
+        if norm:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_F32, nw=nw.cpu(), ss=x.cpu().float().pow(2).sum(-1))
+            torch.testing.assert_close(got, want, rtol=2e-3, atol=2e-3)
+        elif epi == gemv.EPI_RESID:
+            want, _ = O.gemv(x.cpu(), W.cpu(), O.EPI_RESID, h=h0.cpu())
+            assert_resid_close(got, want, y_f32)
+        elif epi == gemv.EPI_BF16:
+            want = O.gemv(x.cpu(), W.cpu(), O.EPI_BF16)
+            assert_bf16_close(got, want, max_ulp=2, max_frac=0.03, atol=one_ulp_at(want))
+        else:
+            torch.testing.assert_close(got, y_f32.float(), rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("M,cfg", [(1, (1, 4, 2)), (1, (0, 8, 0)), (3, (1, 2, 4)), (3, (0, 8, 0)),
                                    (4, (0, 4, 0)), (16, (0, 8, 0)),
                                    (3, (2, 1, 0)), (16, (2, 2, 0)),
