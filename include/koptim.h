@@ -124,19 +124,23 @@ int ko_decode_attn_qkv(const void* qkv, const void* q_w, const void* k_w, const 
 
 /* ko_decode_attn_qkv (with counters) and the o projection with its residual add
  * in ONE launch, for B <= 2 and unit % 64 == 0 (4 wavefronts per unit) and an
- * o-projection input width nq*head_dim <= 4096: out [B, nq*head_dim] receives the merged attention output as before,
- * and h [B, H] <- bf16(h + bf16(out @ w_o^T)) (w_o [H, nq*head_dim] bf16), the
- * RESID GEMV of engine/engine.py:330-331 (kernels/gemv.py EPI_RESID). Extra
+ * o-projection input width nq*head_dim <= 4096: out [B, nq*head_dim] receives
+ * the merged attention output as before, and h [B, H] <- bf16(h + bf16(out @
+ * w_o^T)) (w_o [H, nq*head_dim] bf16), the RESID GEMV of engine/engine.py:330-331
+ * (kernels/gemv.py EPI_RESID), bit-identical to the separate launches. Extra
  * workgroups own 8 columns of the projection each; they load their weights while
- * the attention runs and wait on a device-coherent count of merged (sequence,
- * KV head) pairs. sync: ko_decode_attn_qkv_oproj_sync_ints() int32 (zero before
- * the first call; every call leaves it zero); err [1] int32 is set to 1 if that
- * wait ever gave up (never expected; the results of such a call are invalid).
- * delay_ns: how long the projection workgroups hold their weight loads so the
- * attention's first loads go ahead of them (0: no delay). rope: as for
- * ko_decode_attn_qkv. Replaces
- * engine.py:328-332 (attention, o projection and its residual add); no single
- * reference function. */
+ * the attention runs, and each wavefront reads the slice of the merged output
+ * of a (sequence, KV head) pair once that pair's done flag is raised.
+ * sync: ko_decode_attn_qkv_oproj_sync_ints() int32, 8-byte aligned, zero before
+ * the first call; it carries a launch epoch from call to call (zeroing it again
+ * between calls is allowed). err [1] int32 is set to 1 if a wait gave up
+ * (never expected; the results of such a call are invalid) and stays set until
+ * the caller clears it. spin_max: polls of a done flag before a wait gives up
+ * (< 0: the library's bound, 2^21 polls of ~1 us; 0: give up at once, for tests
+ * of that path). delay_ns: how long the projection workgroups hold their weight
+ * loads so the attention's first loads go ahead of them (0: no delay). rope: as
+ * for ko_decode_attn_qkv. Replaces engine.py:328-332 (attention, o projection
+ * and its residual add); no single reference function. */
 int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, const void* cos,
                              const void* sin, int max_pos, const int* pos, void* k_cache,
                              void* v_cache, int cap, long long cache_b_stride,
@@ -144,7 +148,7 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
                              int max_units, int grid_waves, float eps, float scale,
                              float* o_part, float* ml, int* counters, void* out,
                              const void* w_o, void* h, int H, int* sync, int* err,
-                             int delay_ns, const void* rope, void* stream);
+                             int delay_ns, int spin_max, const void* rope, void* stream);
 
 /* int32 elements of ko_decode_attn_qkv_oproj's sync array (a size, not a status). */
 long long ko_decode_attn_qkv_oproj_sync_ints(void);
@@ -271,14 +275,18 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
  * ring (optional, [ring_rows, M] int64 in pinned host memory): row
  * ring_ctr[m] (int32 on the device, in [0, ring_rows)) receives ids[m] with a
  * system-scope store and ring_ctr[m] advances by one, wrapping to 0; a host
- * that waits for the stream then reads the ids without a copy.
+ * that waits for the stream then reads the ids without a copy. err (optional,
+ * with the ring; int32 on the device): while *err is nonzero (the err flag of
+ * ko_decode_attn_qkv_oproj, set when a wait of that launch gave up and kept
+ * until the caller clears it) the ring receives -2 in place of the ids, so a
+ * host reading the ring sees the failure at the step where it happened.
  * Layouts, scratch (part) and the other arguments as for ko_gemv. */
 int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float* ss, void* logits,
                       long long* ids, int* pos, const void* next_emb, void* next_h,
                       const void* cos, const void* sin, int max_pos, int head_dim, void* rope,
-                      long long* ring, int ring_rows, int* ring_ctr, float* part,
-                      long long part_len, int M, int N, int K, int layout, int rows, int waves,
-                      float eps, void* stream);
+                      long long* ring, int ring_rows, int* ring_ctr, const int* err,
+                      float* part, long long part_len, int M, int N, int K, int layout, int rows,
+                      int waves, float eps, void* stream);
 
 /* Number of fp32 scratch elements ko_gemv needs for N columns with this launch
  * configuration: the ARGMAX partials (epi 4) of layouts 0-2, or layout 3's

@@ -45,8 +45,8 @@ SIGNATURES = {
                 _int, _int, _int, _int, _int, _f, _c_void_p],
     "ko_lm_head_argmax": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                           _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int,
-                          _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _ll, _int, _int, _int,
-                          _int, _int, _int, _f, _c_void_p],
+                          _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _ll, _int,
+                          _int, _int, _int, _int, _int, _f, _c_void_p],
     "ko_gemv_argmax_scratch": [_int, _int, _int, _int],
     "ko_gemv_tile": [_c_void_p, _c_void_p, _int, _int, _c_void_p],
     "ko_argmax_rows": [_c_void_p, _ll, _int, _int, _c_void_p, _c_void_p],
@@ -54,7 +54,7 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _int, _ll, _ll, _int, _int,
                                  _int, _int, _int, _int, _f, _f, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
-                                 _c_void_p, _int, _c_void_p, _c_void_p],
+                                 _c_void_p, _int, _int, _c_void_p, _c_void_p],
     "ko_decode_attn_qkv_oproj_sync_ints": [],
     "ko_decode_attn_noalloc": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _ll, _ll,
                                _int, _int, _int, _int, _int, _int, _int, _f, _c_void_p,

@@ -444,85 +444,183 @@ __global__ __launch_bounds__(64 * WM) void attn1_kernel(AttnArgs a) {
 // Decode attention and the o projection in one launch (one query token, 1-2
 // sequences, 4 wavefronts per unit). Workgroups [0, nattn) run the attention
 // units with the fused combine; the rest each own 8 output columns of the o
-// projection: they issue all their weight loads, wait until every (b, kv_head)
-// pair has been merged (a device-coherent counter), then read the merged
-// attention output with device-scope loads and finish as the RESID GEMV
-// (h <- bf16(h + bf16(W_o attn))). The o-projection weights thus stream while
-// the attention's latency chain runs instead of after it. Workgroups are
-// dispatched in index order, so every attention workgroup is resident before
-// any o-projection workgroup waits; the wait is also bounded (SPIN_MAX polls,
-// then *err is set and the workgroup goes on). The counters re-arm themselves
-// for the next launch once every projection workgroup is done.
+// projection: they issue all their weight loads while the attention's latency
+// chain runs, then finish as the RESID GEMV (h <- bf16(h + bf16(W_o attn))),
+// each wavefront reading a chunk of the merged attention output (device-scope
+// loads) as soon as the done flags of the (sequence, KV head) pairs it covers
+// are raised. Workgroups are dispatched in index order, so every attention
+// workgroup is resident before any o-projection workgroup waits; the waits are
+// also bounded (spin_max polls, then *err is set and the wavefront goes on).
+// Synchronisation words: OPROJ_FLAG0 and what follows it.
 
-// The pair that completes the count of live pairs raises the done flag (one
-// copy per 128-byte line, so its waiters do not queue on one address).
-struct OprojHooks {
-  static constexpr bool kNotify = true;
-  __device__ void merged(const AttnArgs& a, int live) const {
-    const int prev =
-        __hip_atomic_fetch_add(a.pairs_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == live - 1) {
-      for (int f = 0; f < OPROJ_FLAGS; ++f)
-        __hip_atomic_store(a.pairs_done + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * f, 1,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+// The 8-byte word of a workgroup's group: the launch epoch (high half) and the
+// count of the group's workgroups that have been counted this launch (low half).
+// A projection workgroup counts itself at its start (the epoch comes back with
+// the add), an attention workgroup reads the epoch with a plain device-scope
+// load at its start and counts itself at its end, so no atomic sits on the
+// attention's path to its merge. The last workgroup of the group to be counted
+// stores (epoch + 1, 0) for the next launch; by then every workgroup of the
+// group has read the epoch.
+struct OprojGroup {
+  unsigned long long* word = nullptr;
+  int in_grp = 0;
+  __device__ void locate(int* sync, int blk, int nblk) {
+    const int grp = blk % OPROJ_FLAGS;
+    word = reinterpret_cast<unsigned long long*>(sync + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * grp +
+                                                 OPROJ_GROUP_WORD);
+    in_grp = (nblk - grp + OPROJ_FLAGS - 1) / OPROJ_FLAGS;
   }
-  __device__ void no_units() const {}  // the projection workgroups then time out (*err)
+  // The epoch alone (the word's high half, 4 bytes: an 8-byte load whose dead
+  // low half is reused at once makes the compiler wait for every load in flight).
+  __device__ int peek_epoch() const {
+    return __hip_atomic_load(reinterpret_cast<int*>(word) + 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // Count this workgroup; returns the epoch.
+  __device__ int count() const {
+    const unsigned long long old =
+        __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int e = (int)(old >> 32);
+    if ((unsigned)old == (unsigned)(in_grp - 1))
+      __hip_atomic_store(word, (unsigned long long)(unsigned)(e + 1) << 32, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    return e;
+  }
 };
 
-template <bool QKV, int M>
-__global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g, int nattn,
-                                                         int delay_ticks, int* err) {
-  if ((int)blockIdx.x < nattn) {
-    attn1_body<QKV, 4, true>(a, blockIdx.x, nattn, OprojHooks{});
-    return;
+// The attention side: the merging workgroup of pair p raises copy f of p's done
+// flag in line f for every f (one store per lane), so each group of waiters
+// polls its own 128-byte line.
+struct OprojHooks {
+  static constexpr bool kNotify = true;
+  int* sync;
+  int blk, nblk;
+  OprojGroup grp;  // thread 0
+  int epoch = 0;   // thread 0
+  __device__ void begin() {
+    if (threadIdx.x == 0) {
+      grp.locate(sync, blk, nblk);
+      epoch = grp.peek_epoch();
+    }
   }
-  const int wg = blockIdx.x - nattn;
-  const int nog = gridDim.x - nattn;
+  __device__ void merged(const AttnArgs&, int pair) const {  // wavefront 0
+    const int flag = readlane(epoch, 0) + 1;
+    const int l = lane_id();
+    if (l < OPROJ_FLAGS)
+      __hip_atomic_store(sync + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * l + pair, flag,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ void end() {
+    if (threadIdx.x == 0) grp.count();
+  }
+  __device__ void no_units() const {}  // the projection workgroups then give up (*err)
+};
+
+// The o projection (M rows, 8 output columns per workgroup): gemv_row_body's
+// RESID GEMV with R = 8 and two 8-element chunks of K per thread, c = t and
+// c = t + 256. The workgroup issues its weight loads, then wavefront 0 polls the
+// done flags of all M * nkv (sequence, KV head) pairs of its copy (one int per
+// lane, one load per poll) until every one holds this launch's value; then the
+// workgroup reads the merged attention output with device-scope loads. The sums
+// run in gemv_row_body's order, so h is bit-identical to attention followed by
+// the separate RESID GEMV.
+template <int M>
+__device__ void oproj_body(const GemvArgs& g, int wg, int nkv, int* sync, int* err,
+                           int delay_ticks, int spin_max) {
+  constexpr int R = 8, CPT = 2;
+  __shared__ float red[16][M * R];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int n0 = wg * R;
+  const int N = g.N, K = g.K, KC = K >> 3, mr = g.mrows;
   // Let the attention's first (latency-critical) loads go ahead of this
   // workgroup's weight stream: a short wait on the real-time counter.
   if (delay_ticks > 0) {
     const unsigned long long t0 = wall_clock64();
     while (wall_clock64() - t0 < (unsigned long long)delay_ticks) __builtin_amdgcn_s_sleep(4);
   }
-  const int grp = wg % OPROJ_FLAGS;
-  int* flag = a.pairs_done + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * grp;
-  bool timed_out = false;  // thread 0 only
-  auto wait_x = [&] {
-    if (threadIdx.x == 0) {
-      int it = 0;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-        __builtin_amdgcn_s_sleep(8);
-        if (++it >= SPIN_MAX) {
-          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          timed_out = true;
-          break;
-        }
-      }
-    }
-    __syncthreads();
-  };
-  gemv_row_body<M, 8, false, EPI_RESID, 2, true>(g, wg, wait_x);
-  // Re-arm for the next launch, off the critical path: the last workgroup of a
-  // flag group clears that flag and counts the group; the last group clears the
-  // pair count and the group count. A workgroup whose wait gave up does not
-  // count itself: its group then never re-arms, so a merge that arrives late
-  // cannot be taken for the next launch's, and *err stays set until the host
-  // clears the sync words with it.
-  if (threadIdx.x == 0 && !timed_out) {
-    const int in_grp = (nog - grp + OPROJ_FLAGS - 1) / OPROJ_FLAGS;  // workgroups of group grp
-    if (__hip_atomic_fetch_add(flag + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-        in_grp - 1) {
-      __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(flag + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int groups = nog < OPROJ_FLAGS ? nog : OPROJ_FLAGS;
-      if (__hip_atomic_fetch_add(a.pairs_done + 1, 1, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) == groups - 1) {
-        __hip_atomic_store(a.pairs_done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.pairs_done + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+  uint16_t hpre;  // this thread's residual element, issued before the weights
+  {
+    const int ti = t < M * R ? t : 0;
+    hpre = resid_load(g, ti / R, n0 + ti % R);
   }
+  uint4 w[CPT][R];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = min(t + GEMV_NT * j, KC - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[j][r] = ldg16_stream(g.w + (long long)min(n0 + r, N - 1) * K + 8 * c);
+  }
+  if (wv == 0) {
+    int e = 0;
+    if (lane == 0) {
+      OprojGroup grp;
+      grp.locate(sync, blockIdx.x, gridDim.x);
+      e = grp.count();
+    }
+    const int flag = readlane(e, 0) + 1;
+    const int npairs = mr * nkv;  // <= OPROJ_MAX_PAIRS
+    const int* fp = sync + OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * (blockIdx.x % OPROJ_FLAGS) +
+                    (lane < npairs ? lane : 0);
+    // One poll in flight with a short sleep between polls: more polls in flight
+    // (four, a quarter round trip apart) measured slower, as they load the flag
+    // lines and the merges' coherent traffic.
+    bool ok = false;
+    for (int it = 0; it < spin_max; ++it) {
+      const int v = __hip_atomic_load(fp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__ballot(lane < npairs && v != flag) == 0) {
+        ok = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+    if (!ok && lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  uint4 x[CPT][M];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = t + GEMV_NT * j;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      x[j][m] = c < KC && m < mr ? ldg16_coherent(g.x + (long long)m * K + 8 * c) : zero;
+  }
+  float acc[M][R];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][r] = dot8(x[j][m], w[j][r], j == 0 ? 0.f : acc[m][r]);
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = row_sum16(acc[m][r]);
+      if ((lane & 15) == 0) red[wv * 4 + (lane >> 4)][m * R + r] = v;
+    }
+  __syncthreads();
+  if (t < M * R) {
+    const int m = t / R, r = t - (t / R) * R, n = n0 + r;
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tot += red[i][m * R + r];
+    if (m < mr && n < N) epilogue<EPI_RESID>(g, m, n, tot, 0.f, &hpre);
+  }
+}
+
+template <bool QKV, int M>
+__global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, GemvArgs g, int nattn,
+                                                         int delay_ticks, int spin_max, int* err) {
+  if ((int)blockIdx.x < nattn) {
+    OprojHooks hooks;
+    hooks.sync = a.pairs_done;
+    hooks.blk = blockIdx.x;
+    hooks.nblk = gridDim.x;
+    attn1_body<QKV, 4, true>(a, blockIdx.x, nattn, hooks);
+    return;
+  }
+  oproj_body<M>(g, blockIdx.x - nattn, a.nkv, a.pairs_done, err, delay_ticks, spin_max);
 }
 
 // Second pass when no counters are given: one wavefront per output row.
@@ -767,7 +865,7 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
                              int max_units, int grid_waves, float eps, float scale,
                              float* o_part, float* ml, int* counters, void* out,
                              const void* w_o, void* h, int H, int* sync, int* err,
-                             int delay_ns, const void* rope, void* stream) {
+                             int delay_ns, int spin_max, const void* rope, void* stream) {
   int st = check_common(k_cache, v_cache, pos, cap, cache_b_stride, cache_h_stride, B, 1, nkv,
                         head_dim, unit, max_units, o_part, ml);
   if (st) return st;
@@ -776,11 +874,12 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
     return KO_EINVAL;
   if (!aligned16(qkv) || !aligned16(q_w) || !aligned16(k_w) || !aligned16(cos) ||
       !aligned16(sin) || !aligned16(out) || !aligned16(w_o) || !aligned16(h) ||
-      (rope && !aligned16(rope)))
+      (rope && !aligned16(rope)) || (reinterpret_cast<uintptr_t>(sync) & 7u))
     return KO_EINVAL;
   if (B > 2 || waves_per_unit(unit) != 4) return KO_ENOTSUP;
   const int K = nkv * G * D;  // o projection input width
-  if (K > 2 * GEMV_NT * 8) return KO_ENOTSUP;
+  if (K > 2 * GEMV_NT * 8 || B * nkv > OPROJ_MAX_PAIRS) return KO_ENOTSUP;
+  if (spin_max < 0) spin_max = SPIN_MAX;
   AttnArgs a = base_args(k_cache, v_cache, pos, 1, cap, cache_b_stride, cache_h_stride, B, nkv,
                          unit, max_units, scale, o_part, ml);
   a.qkv = static_cast<const uint16_t*>(qkv);
@@ -807,9 +906,11 @@ int ko_decode_attn_qkv_oproj(const void* qkv, const void* q_w, const void* k_w, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int ticks = delay_ns > 0 ? delay_ns / 10 : 0;  // s_memrealtime runs at 100 MHz
   if (B == 1)
-    hipLaunchKernelGGL((attn_oproj_kernel<true, 1>), grid, block, 0, s, a, g, nattn, ticks, err);
+    hipLaunchKernelGGL((attn_oproj_kernel<true, 1>), grid, block, 0, s, a, g, nattn, ticks,
+                       spin_max, err);
   else
-    hipLaunchKernelGGL((attn_oproj_kernel<true, 2>), grid, block, 0, s, a, g, nattn, ticks, err);
+    hipLaunchKernelGGL((attn_oproj_kernel<true, 2>), grid, block, 0, s, a, g, nattn, ticks,
+                       spin_max, err);
   return KO_LAUNCH_STATUS();
 }
 

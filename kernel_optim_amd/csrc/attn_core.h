@@ -19,11 +19,21 @@ constexpr float TAU = 8.0f;     // lazy-rescale threshold, log2 units
 constexpr float NEG_BIG = -1.0e30f;
 
 constexpr int SPIN_MAX = 1 << 21;
-// sync[] layout of ko_decode_attn_qkv_oproj: [0] merged-pair count, [1] projection
-// workgroups past their wait, then OPROJ_FLAGS done-flag copies 128 bytes apart.
-// Each flag line also carries, one int further on, the count of projection
-// workgroups of that flag's group that have finished (re-arm bookkeeping).
+// sync[] of ko_decode_attn_qkv_oproj (all zero before the first launch): OPROJ_FLAGS
+// lines of 128 bytes from int OPROJ_FLAG0 on, one per group of workgroups
+// (workgroup w of the launch belongs to group w % OPROJ_FLAGS). Line f holds
+//   - ints [0, OPROJ_MAX_PAIRS): copy f of the done flag of each (sequence, KV
+//     head) pair p = b * nkv + kv_head, which the pair's merging workgroup sets
+//     to E + 1 once the pair's merged output is performed;
+//   - the 8-byte word at int OPROJ_GROUP_WORD: the group's launch epoch E (high
+//     half) and the count of its workgroups counted so far (low half).
+// Every workgroup reads E from its group word before it uses it and counts
+// itself in the word once; the last one counted sets the word to (E + 1, 0).
+// Each launch thus waits for flags equal to E + 1 where the launch before set
+// E, so a flag left by an earlier launch never reads as set and no flag is
+// ever cleared.
 constexpr int OPROJ_FLAG0 = 32, OPROJ_FLAG_STRIDE = 32, OPROJ_FLAGS = 32;
+constexpr int OPROJ_MAX_PAIRS = 16, OPROJ_GROUP_WORD = 16;
 constexpr int OPROJ_SYNC_INTS = OPROJ_FLAG0 + OPROJ_FLAG_STRIDE * OPROJ_FLAGS;
 
 constexpr int MAX_T = 8;  // query tokens per sequence of one attention call
@@ -245,18 +255,21 @@ __device__ __forceinline__ uint32_t norm_rope2(uint32_t x, uint32_t w, uint32_t 
 // Hooks: what a launch that holds the consumer of the merged output adds
 // (NoAttnHooks: nothing). kNotify (with FUSED): the merged output is read later
 // in the same launch: it is stored device-coherently, and once a pair's merged
-// rows are performed thread 0 calls merged(a, live_pairs) (live_pairs counts
-// the (b, kv_head) pairs with keys; 1-64 sequences). no_units() runs on
-// workgroup 0 when no sequence has a key (then nothing is merged).
+// rows are performed wavefront 0 calls merged(a, pair) with the pair's index
+// b * nkv + kv_head. begin() runs once per workgroup after its first loads are
+// issued, end() once after its last unit; no_units() runs on workgroup 0 when
+// no sequence has a key (then nothing is merged).
 struct NoAttnHooks {
   static constexpr bool kNotify = false;
+  __device__ void begin() {}
   __device__ void merged(const AttnArgs&, int) const {}
+  __device__ void end() {}
   __device__ void no_units() const {}
 };
 
 template <bool QKV, int WM, bool FUSED, class Hooks = NoAttnHooks>
 __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
-                                           const Hooks& hooks = Hooks{}) {
+                                           Hooks hooks = Hooks{}) {
   static_assert(!Hooks::kNotify || FUSED, "a consumer in the launch reads the merged output");
   __shared__ int lds_prev;
   __shared__ __align__(16) uint16_t lds_p[WM][G * 16];
@@ -314,6 +327,7 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
         va[s4] = ldg16_stream(vb + (long long)min(k0 + g + 4 * s4, klim) * D + 8 * r);
     }
   }
+  hooks.begin();
 
   const bool small_b = a.B <= 64;
   int my_n = 0, my_incl = 0, total, len1 = 0, my_len = 0;  // lane b: sequence b (B <= 64)
@@ -689,16 +703,14 @@ __device__ __forceinline__ void attn1_body(const AttnArgs& a, int wg, int nwg,
         if constexpr (Hooks::kNotify) {
           __builtin_amdgcn_s_waitcnt(0);  // this wave's merged row is performed
           __syncthreads();
+          if (wave == 0) hooks.merged(a, b * nkv + kvh);
         }
-        [[maybe_unused]] const int live_pairs = __popcll(__ballot(my_n > 0)) * nkv;
-        if (threadIdx.x == 0) {
-          __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if constexpr (Hooks::kNotify) hooks.merged(a, live_pairs);
-        }
+        if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __syncthreads();  // the next unit reuses the LDS
   }
+  hooks.end();
 }
 
 

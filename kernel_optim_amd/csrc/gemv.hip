@@ -75,7 +75,8 @@ __global__ __launch_bounds__(256) void gemv_tile_kernel(const uint16_t* __restri
 // embedding gather, gemv.py:201-211, so the next step needs no gather launch),
 // and the rest of the decode step's tail (StepTail): the RoPE rows of the new
 // position for the next step's attention, and the id written straight into a
-// ring in pinned host memory (no device-to-host copy per token).
+// ring in pinned host memory (no device-to-host copy per token), or -2 there
+// when the step's attention + o projection launches report a failed wait.
 constexpr int FT = 1024;
 
 struct StepTail {
@@ -89,6 +90,9 @@ struct StepTail {
   long long* ring;
   int ring_rows, ring_ld;
   int* ring_ctr;
+  // with the ring: nonzero *err (a failed wait of ko_decode_attn_qkv_oproj,
+  // left set until the host clears it) stores -2 in place of the id
+  const int* err;
 };
 __device__ __forceinline__ void better(float v, int i, float& bv, int& bi) {
   if (v > bv || (v == bv && i < bi)) {
@@ -130,6 +134,9 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
   __shared__ int s_id, s_pos;
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const float2* pr = part + (long long)m * nparts;
+  int failed = 0;  // thread 0, issued ahead of the partials
+  if (t == 0 && tail.ring && tail.err)
+    failed = __hip_atomic_load(tail.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int i0 = t; i0 < nparts; i0 += FL * FT) {
@@ -175,8 +182,9 @@ __global__ __launch_bounds__(FT) void argmax_finalize_kernel(
       // rows of the ring live in pinned host memory: a system-scope store
       const int c = tail.ring_ctr[m];
       const int slot = c >= 0 && c < tail.ring_rows ? c : 0;
-      __hip_atomic_store(tail.ring + (long long)slot * tail.ring_ld + m, (long long)i,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(tail.ring + (long long)slot * tail.ring_ld + m,
+                         failed ? -2LL : (long long)i, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
       tail.ring_ctr[m] = slot + 1 < tail.ring_rows ? slot + 1 : 0;
     }
   }
@@ -381,9 +389,9 @@ int ko_gemv(const void* x, const void* w, void* y, const void* nw, const float* 
 int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float* ss, void* logits,
                       long long* ids, int* pos, const void* next_emb, void* next_h,
                       const void* cos, const void* sin, int max_pos, int head_dim, void* rope,
-                      long long* ring, int ring_rows, int* ring_ctr, float* part,
-                      long long part_len, int M, int N, int K, int layout, int rows, int waves,
-                      float eps, void* stream) {
+                      long long* ring, int ring_rows, int* ring_ctr, const int* err,
+                      float* part, long long part_len, int M, int N, int K, int layout, int rows,
+                      int waves, float eps, void* stream) {
   StepTail tail = {};
   if (rope) {
     if (!pos || !cos || !sin || max_pos < 1 || head_dim < 8 || (head_dim & 7)) return KO_EINVAL;
@@ -400,6 +408,7 @@ int ko_lm_head_argmax(const void* x, const void* w, const void* nw, const float*
     tail.ring_rows = ring_rows;
     tail.ring_ld = M;
     tail.ring_ctr = ring_ctr;
+    tail.err = err;
   }
   return gemv_impl(x, w, logits, nw, ss, nullptr, nullptr, ids, pos, next_emb, next_h, part,
                    part_len, M, N, K, EPI_ARGMAX, nw != nullptr, 0, layout, rows, waves, eps,

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(NT) void gemv_block_kernel(GemvArgs a) {
 
 template <int M, int R, bool NORM, int EPI, int CPT>
 __global__ __launch_bounds__(NT) void gemv_row_kernel(GemvArgs a) {
-  gemv_row_body<M, R, NORM, EPI, CPT, false>(a, blockIdx.x, [] {});
+  gemv_row_body<M, R, NORM, EPI, CPT>(a, blockIdx.x);
 }
 
 template <int M, int R, int CPT>

@@ -95,15 +95,10 @@ __device__ __forceinline__ float epilogue(const GemvArgs& a, int m, int n, float
 // issued; loads return in issue order, so a dot product never waits behind a
 // later load. Chunk indices past K are clamped to a valid chunk whose x is
 // zeroed, which keeps the loads unconditional and the wait counts exact.
-// CPT = chunks of 8 per thread (K <= 2048 * CPT).
-// XCOH: x was written earlier in the same launch by other workgroups through
-// device-coherent stores; read it with device-scope loads. wg: this workgroup's
-// column group.
-//
-// With XCOH the weights are issued first and `wait_x()` runs before x is read:
-// the caller's wait for the producer of x then overlaps the weight stream.
-template <int M, int R, bool NORM, int EPI, int CPT, bool XCOH, class WaitX>
-__device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&& wait_x) {
+// CPT = chunks of 8 per thread (K <= 2048 * CPT). wg: this workgroup's column
+// group.
+template <int M, int R, bool NORM, int EPI, int CPT>
+__device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg) {
   constexpr int NW = EPI == EPI_SWIGLU ? 2 * R : R;
   __shared__ float red[16][M * NW];
   __shared__ float s_sq[GEMV_NT / 64][M];
@@ -122,9 +117,7 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
       const int c = min(t + GEMV_NT * j, KC - 1);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const uint16_t* xp = a.x + (long long)(m < mr ? m : 0) * K + 8 * c;
-        if constexpr (XCOH) xr[m][j] = ldg16_coherent(xp);
-        else xr[m][j] = ldg16(xp);
+        xr[m][j] = ldg16(a.x + (long long)(m < mr ? m : 0) * K + 8 * c);
       }
       if constexpr (NORM) nwr[j] = ldg16(a.nw + 8 * c);
     }
@@ -136,7 +129,7 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
     const int ti = t < M * R ? t : 0;
     hpre = resid_load(a, ti / R, n0 + ti % R);
   }
-  if constexpr (!XCOH) load_x();
+  load_x();
   uint4 w[CPT][NW];
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
@@ -146,10 +139,6 @@ __device__ __forceinline__ void gemv_row_body(const GemvArgs& a, int wg, WaitX&&
       const int n = r < R ? min(n0 + r, N - 1) : N + min(n0 + r - R, N - 1);
       w[j][r] = ldg16_stream(a.w + (long long)n * K + 8 * c);
     }
-  }
-  if constexpr (XCOH) {
-    wait_x();
-    load_x();
   }
   const uint4 zero = make_uint4(0, 0, 0, 0);
 #pragma unroll

@@ -60,11 +60,16 @@ ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 # units per sequence of the one-token attention at B >= 3 (-1: one round of the
 # 256 CUs, 256 // (B * KV heads); 0: fixed units of ATTN_UNIT or the sizing rule)
 ATTN_SPLIT = int(os.environ.get("ENGINE_ATTN_SPLIT", "-1"))
-# decode-step graph: "auto" captures the fused-GEMV step and the hipBLASLt step for
-# batches up to FUSED_MAX_B and keeps the faster (engine.py:197-208); "fused" or
+# decode-step graph: "auto" takes the fused-GEMV step up to FUSED_MAX_B sequences
+# and the hipBLASLt step above; "timed" captures both up to FUSED_MAX_TIMED and
+# keeps the faster, as the reference does (engine.py:197-208); "fused" or
 # "hipblaslt" takes one
 DECODE_GRAPH = os.environ.get("ENGINE_DECODE_GRAPH", "auto")
-FUSED_MAX_B = 64     # fused-GEMV decode up to this batch; hipBLASLt beyond (engine.py:44)
+# The fused GEMVs read each weight once for up to 32 rows (B = 32: 8,619 tok/s
+# against 7,544 on hipBLASLt); at 33..64 rows qkv, gate/up and the LM head take
+# two weight passes (B = 64: 9,538 against 11,599 tok/s on hipBLASLt).
+FUSED_MAX_B = 32
+FUSED_MAX_TIMED = 64  # "timed": both graphs up to here (engine.py:44)
 # verify-step attention: the K+1 tokens of a sequence as rows of the one-token
 # kernel (one launch) rather than T-token tiles (two launches and a merge)
 VERIFY_TOKEN_ROWS = os.environ.get("ENGINE_VERIFY_TOKEN_ROWS", "1") == "1"
@@ -258,15 +263,16 @@ class Engine:
 
     def _init(self, cfg, w, keep_logits, spec=None, decode_graph=None):
         """spec: prompt-lookup speculation on (True) or off (False); None takes
-        ENGINE_SPEC (off unless set to 1). decode_graph: "auto" (time the fused
-        and the hipBLASLt decode graphs at setup and keep the faster; hipBLASLt
-        alone above FUSED_MAX_B), "fused" or "hipblaslt"; None takes
+        ENGINE_SPEC (off unless set to 1). decode_graph: "auto" (the fused-GEMV
+        decode graph up to FUSED_MAX_B sequences, the hipBLASLt graph above),
+        "timed" (capture both up to FUSED_MAX_TIMED sequences, time them at setup
+        and keep the faster), "fused" or "hipblaslt"; None takes
         ENGINE_DECODE_GRAPH (auto unless set)."""
         self.spec = SPEC if spec is None else bool(spec)
         self.min_advance = MIN_ADVANCE   # None: the measured break-even
         kind = DECODE_GRAPH if decode_graph is None else decode_graph
-        if kind not in ("auto", "fused", "hipblaslt"):
-            raise ValueError(f"decode_graph must be auto, fused or hipblaslt, not {kind!r}")
+        if kind not in ("auto", "timed", "fused", "hipblaslt"):
+            raise ValueError(f"decode_graph must be auto, timed, fused or hipblaslt, not {kind!r}")
         self.decode_graph = kind
         if cfg.head_dim != 128 or cfg.nq != 4 * cfg.nkv:
             raise ValueError("the decode kernels serve head_dim 128 with 4 query heads per KV head")
@@ -276,6 +282,10 @@ class Engine:
         self._shape = None
         self.g1 = None
         self._tile_cache = {}
+        # polls of a done flag before an attention + o projection wait gives up
+        # (-1: the library's bound; 0: at once, which tests of that path use);
+        # taken at the next setup
+        self.oproj_spin = -1
 
     # ------------------------------------------------------------------ setup
     def _tables(self, n):
@@ -321,20 +331,23 @@ class Engine:
                                     unit=ATTN_UNIT or None, fused_combine=True,
                                     units_per_seq=attn_units_per_seq(B, cfg.nkv))
         self.attn.oproj_delay_ns = OPROJ_DELAY_NS
+        self.attn.oproj_spin = self.oproj_spin
         L = self.w["layers"]
         raw = dict(qkv=[l["qkv"] for l in L], o=[l["o"] for l in L], gu=[l["gu"] for l in L],
                    down=[l["down"] for l in L], lm=[self.w["lm_head"]])
         deadline = time.monotonic() + TUNE_BUDGET_S
         kind = self.decode_graph
-        if kind == "auto" and B > FUSED_MAX_B:
+        if kind == "auto":
+            kind = "fused" if B <= FUSED_MAX_B else "hipblaslt"
+        elif kind == "timed" and B > FUSED_MAX_TIMED:
             kind = "hipblaslt"
         self.step_times = {}
         g_fused = g_mm = None
-        if kind in ("auto", "fused"):
+        if kind in ("timed", "fused"):
             g_fused = self._setup_fused(raw, deadline)
-        if kind in ("auto", "hipblaslt"):
+        if kind in ("timed", "hipblaslt"):
             g_mm = self._setup_mm()
-        if kind == "auto":
+        if kind == "timed":
             # keep whichever decode graph is faster here, measured during setup
             t_f = min(self._time_graph(g_fused) for _ in range(2))
             t_m = min(self._time_graph(g_mm) for _ in range(2))
@@ -462,7 +475,8 @@ class Engine:
         # rows + the ids into the pinned host ring, in one call
         g["lm"](h, W["lm"][0], y=self.logits, nw=self.w["final_norm"], ids=self.ids,
                 pos_inc=self.pos, next_emb=self.w["embed"], next_h=h,
-                rope=(self._cos, self._sin, self.rope), ring=(self.pin_ids, self.ring_ctr))
+                rope=(self._cos, self._sin, self.rope),
+                ring=(self.pin_ids, self.ring_ctr, self.attn.err if fuse_o else None))
 
     def _step1_mm(self):
         """One decode token per sequence with hipBLASLt GEMMs (torch.mm) between
@@ -603,61 +617,70 @@ class Engine:
         if N <= 0:
             return
         B, S = len(input_ids), len(input_ids[0])
+        # nothing from an earlier call may still write the ring or the caches
+        torch.cuda.synchronize()
         self._setup(B, S, N)
         stream = torch.cuda.current_stream()
-        prompt = torch.tensor(input_ids, dtype=torch.int64).pin_memory().to(DEVICE,
-                                                                            non_blocking=True)
-        self._prefill(prompt)
-        ids_h, ev = self.pin_ids, self.events
-        ids_h[0].copy_(self.ids, non_blocking=True)
-        ev[0].record(stream)
-        if self.K:
-            yield from self._generate_spec(input_ids, N, stream)
-            return
-        # The fused step writes its ids into row ring_ctr of ids_h itself, so the
-        # host waits for row j to fill (rows start at -1) instead of recording
-        # an event per step; the hipBLASLt step's ids are copied after each
-        # replay and waited for with an event.
-        ring = self.step_kind == "fused"
-        if ring:
-            self._ring_np[1:] = -1
-            self.ring_ctr.fill_(1)
-        # Keep one replay in flight: queue step j before waiting for step j-1.
-        if N > 1:
-            self.g1.replay()
-            if not ring:
-                ids_h[1].copy_(self.ids, non_blocking=True)
-                ev[1].record(stream)
-        ev[0].synchronize()
-        yield ids_h[0].tolist()
-        for j in range(1, N):
-            if j + 1 < N:
+        try:
+            prompt = torch.tensor(input_ids, dtype=torch.int64).pin_memory().to(
+                DEVICE, non_blocking=True)
+            self._prefill(prompt)
+            ids_h, ev = self.pin_ids, self.events
+            ids_h[0].copy_(self.ids, non_blocking=True)
+            ev[0].record(stream)
+            if self.K:
+                yield from self._generate_spec(input_ids, N, stream)
+                return
+            # The fused step writes its ids into row ring_ctr of ids_h itself, so
+            # the host waits for row j to fill (rows start at -1) instead of
+            # recording an event per step; the hipBLASLt step's ids are copied
+            # after each replay and waited for with an event.
+            ring = self.step_kind == "fused"
+            if ring:
+                self._ring_np[1:] = -1
+                self.ring_ctr.fill_(1)
+            # Keep one replay in flight: queue step j before waiting for step j-1.
+            if N > 1:
                 self.g1.replay()
                 if not ring:
-                    ids_h[j + 1].copy_(self.ids, non_blocking=True)
-                    ev[j + 1].record(stream)
-            if ring:
-                self._wait_row(j)
-            else:
-                ev[j].synchronize()
-            if j == N - 1:
-                self.attn.check_sync()   # raises if a fused o-projection wait gave up
-            yield ids_h[j].tolist()
+                    ids_h[1].copy_(self.ids, non_blocking=True)
+                    ev[1].record(stream)
+            ev[0].synchronize()
+            yield ids_h[0].tolist()
+            for j in range(1, N):
+                if j + 1 < N:
+                    self.g1.replay()
+                    if not ring:
+                        ids_h[j + 1].copy_(self.ids, non_blocking=True)
+                        ev[j + 1].record(stream)
+                if ring:
+                    self._wait_row(j)   # raises at the step whose o-projection wait failed
+                else:
+                    ev[j].synchronize()
+                yield ids_h[j].tolist()
+            self.attn.check_sync()
+        finally:
+            # a caller that stops early (or an error) leaves no replay in flight
+            torch.cuda.synchronize()
 
     def _wait_row(self, j, timeout_s=60.0):
         """Wait until the decode step that writes row j of the pinned id ring has
         stored every sequence's id (the LM head's tail stores them from the GPU;
-        the rows start at -1)."""
+        the rows start at -1). A row of -2 is a step whose attention + o
+        projection wait gave up: raise (DecodeAttention.check_sync) at that step."""
         row = self._ring_np[j]
-        if (row >= 0).all():
-            return
-        t_end = time.monotonic() + timeout_s
-        while not (row >= 0).all():
-            if time.monotonic() > t_end:
+        t_end = None
+        while (row == -1).any():
+            if t_end is None:
+                t_end = time.monotonic() + timeout_s
+            elif time.monotonic() > t_end:
                 torch.cuda.synchronize()
-                if (row >= 0).all():
-                    return
-                raise RuntimeError(f"decode step {j} stored no ids in the host ring")
+                if (row == -1).any():
+                    raise RuntimeError(f"decode step {j} stored no ids in the host ring")
+        if (row < 0).any():
+            torch.cuda.synchronize()
+            self.attn.check_sync()
+            raise RuntimeError(f"decode step {j}: the ring holds no ids")
 
     def _generate_spec(self, input_ids, N, stream):
         """generate() with prompt-lookup speculation (engine.py:435-508): verify
@@ -733,9 +756,13 @@ class Engine:
 
     def _drain(self, j, outs, N, emitted, last=False):
         self.events[j].synchronize()
-        if last:
+        row = self.pin_ids[j].tolist()
+        if last or min(row) < 0:   # -2: that step's o-projection wait gave up
+            torch.cuda.synchronize()
             self.attn.check_sync()
-        for b, t in enumerate(self.pin_ids[j].tolist()):
+            if min(row) < 0:
+                raise RuntimeError(f"decode step {j}: the ring holds no ids")
+        for b, t in enumerate(row):
             outs[b].append(t)
         ready = min(N, min(len(o) for o in outs))
         while emitted < ready:
@@ -758,5 +785,5 @@ class Engine:
             self.g1.replay()
             toks.append(self.ids.cpu())
             logits.append(self.logits.cpu())
-        self.attn.check_sync()
+            self.attn.check_sync()   # raises at the step whose o-projection wait failed
         return torch.stack(toks, 1), logits

@@ -52,6 +52,33 @@ def _check_cache(t, name, B, nkv, cap, d):
 # ---------------------------------------------------------------------------
 # Split-K GQA decode attention (fused.py:130-234).
 # ---------------------------------------------------------------------------
+def attn_geometry(B, T, cap, nkv, target_ctas=2048, unit=None, token_rows=False,
+                  units_per_seq=0):
+    """Launch geometry of DecodeAttention: (keys per unit, units per (sequence, KV
+    head) that the partials are sized for, wavefronts per unit, grid in
+    wavefronts). The reference sizes its split the same way, from the cache
+    length over the programs it wants in flight (fused.py:209-218)."""
+    wg_split = T == 1 or token_rows
+    rows_k = B * T if token_rows else B  # rows the one-token kernel sizes for
+    if unit is None:
+        share = _cdiv(_cdiv(rows_k * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
+        # one-token units stop at 4096 keys (the kernel deals several rounds
+        # of units out largest first, so ragged lengths still fill the
+        # rounds evenly; 4096 against 2048 keys: +1-4.5 % at B = 8-64,
+        # 4096-32768 keys, and ragged B = 64 6,508 against 6,277 GB/s)
+        unit = 4 * max(16, min(1024, share)) if wg_split else max(64, min(1024, share))
+        # ... unless one unit of 2048-4096 keys per CU covers the whole cache:
+        # then a single round of equal units, with the fewest partials to merge
+        per_cu = _cdiv(_cdiv(rows_k * nkv * cap, max(1, target_ctas // 8)), 64) * 64
+        if wg_split and 2048 <= per_cu <= 4096:
+            unit = per_cu
+    max_units = _cdiv(cap, unit)
+    # wavefronts per unit: the kernel's rule (attention.hip, waves_per_unit)
+    wpu = (4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1) if wg_split else 1
+    units = min(max_units, units_per_seq) if units_per_seq else max_units
+    return unit, max_units, wpu, max(1, min(rows_k * nkv * units * wpu, target_ctas))
+
+
 class DecodeAttention:
     """Preallocated split-K attention for T query tokens per sequence, fixed (B, T, cap).
 
@@ -84,8 +111,6 @@ class DecodeAttention:
         # token_rows: the T tokens of a sequence run as T rows of the one-token
         # kernel (ko_decode_attn_token_rows), each with its own causal length
         self.token_rows = bool(token_rows)
-        wg_split = T == 1 or self.token_rows
-        rows_k = B * T if self.token_rows else B  # rows the one-token kernel sizes for
         # units_per_seq = U > 0: decode_qkv cuts each sequence's keys into at most U
         # equal units (multiples of 64 keys, at least `unit`) from its length at
         # each step, so a batch of equal lengths fills one round of the grid
@@ -97,34 +122,16 @@ class DecodeAttention:
                   "the fused combine")
             unit = 64 if unit is None else unit
             _need(unit % 64 == 0, "units_per_seq needs a unit (the smallest unit) % 64 == 0")
-        if unit is None:
-            share = _cdiv(_cdiv(rows_k * nkv * cap, target_ctas), 16) * 16  # keys per wavefront
-            # one-token units stop at 4096 keys (the kernel deals several rounds
-            # of units out largest first, so ragged lengths still fill the
-            # rounds evenly; 4096 against 2048 keys: +1-4.5 % at B = 8-64,
-            # 4096-32768 keys, and ragged B = 64 6,508 against 6,277 GB/s)
-            unit = 4 * max(16, min(1024, share)) if wg_split else max(64, min(1024, share))
-            # ... unless one unit of 2048-4096 keys per CU covers the whole cache:
-            # then a single round of equal units, with the fewest partials to merge
-            per_cu = _cdiv(_cdiv(rows_k * nkv * cap, max(1, target_ctas // 8)), 64) * 64
-            if wg_split and 2048 <= per_cu <= 4096:
-                unit = per_cu
-        _need(unit % 16 == 0 and unit >= 16, "unit must be a positive multiple of 16")
-        self.unit = unit
-        self.max_units = _cdiv(cap, unit)
-        # wavefronts per unit: the kernel's rule (attention.hip, waves_per_unit)
-        if not wg_split:
-            wpu = 1
-        else:
-            wpu = 4 if unit % 64 == 0 else 2 if unit % 32 == 0 else 1
-        self.waves_per_unit = wpu
-        units = min(self.max_units, self.units_per_seq) if self.units_per_seq else self.max_units
-        self.grid_waves = max(1, min(rows_k * nkv * units * wpu, target_ctas))
+        _need(unit is None or (unit % 16 == 0 and unit >= 16),
+              "unit must be a positive multiple of 16")
+        self.unit, self.max_units, self.waves_per_unit, self.grid_waves = attn_geometry(
+            B, T, cap, nkv, target_ctas, unit, self.token_rows, self.units_per_seq)
         rows = B * T * nq
         self.o_part = torch.empty(rows * self.max_units * d, dtype=torch.float32, device=device)
         self.ml = torch.empty(rows * self.max_units * 2, dtype=torch.float32, device=device)
         # per-(sequence or token row, KV head) arrival counters; every launch leaves
         # them at zero
+        rows_k = B * T if self.token_rows else B  # rows of the one-token kernel
         self.counters = (torch.zeros(rows_k * nkv, dtype=torch.int32, device=device)
                          if fused_combine else None)
         # decode_qkv_oproj: its counters and done flags, and its wait-failure flag
@@ -132,6 +139,9 @@ class DecodeAttention:
                                 device=device)
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
         self.oproj_delay_ns = 1000
+        # polls of a pair's done flag before a decode_qkv_oproj wait gives up and
+        # sets err (-1: the library's bound; 0: give up at once, for tests)
+        self.oproj_spin = -1
         self.scale = d ** -0.5
 
     def _check_kv(self, k_cache, v_cache, lens):
@@ -178,8 +188,8 @@ class DecodeAttention:
         """Raise RuntimeError if a decode_qkv_oproj launch since the last check gave
         up its wait for the attention (its results are then invalid). Reads one
         int32 from the device, so it synchronises; before raising it clears the
-        sync words, the arrival counters and the flag, so the next launch starts
-        clean."""
+        sync words, the arrival counters and the flag (zeroed sync words are a
+        valid start), so the next launch starts clean."""
         if int(self.err.item()) == 0:
             return
         torch.cuda.synchronize(self.err.device)
@@ -232,7 +242,7 @@ class DecodeAttention:
                   self.unit, self.max_units, self.grid_waves, eps, self.scale,
                   _lib.ptr(self.o_part), _lib.ptr(self.ml), _lib.ptr(self.counters), _lib.ptr(out),
                   _lib.ptr(w_o), _lib.ptr(h), H, _lib.ptr(self.sync), _lib.ptr(self.err),
-                  self.oproj_delay_ns, _lib.ptr(rope), _lib.stream_ptr())
+                  self.oproj_delay_ns, self.oproj_spin, _lib.ptr(rope), _lib.stream_ptr())
 
     def decode_qkv(self, qkv, q_w, k_w, cos, sin, pos, k_cache, v_cache, out, eps, rope=None):
         """Decode step (T=1) straight from the bf16 QKV projection [B, (nq+2nkv)*d]:

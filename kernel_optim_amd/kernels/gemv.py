@@ -167,7 +167,8 @@ class Gemv:
         RoPE rows of the advanced positions into out ([M, 2, d] bf16, what
         rope_rows writes), and ``ring = (host, ctr)`` stores the ids into row
         ctr[m] of host ([R, M] int64, pinned) and advances ctr ([M] int32 on the
-        device) modulo R."""
+        device) modulo R; ``ring = (host, ctr, err)`` stores -2 in place of the
+        ids while err ([1] int32 on the device, DecodeAttention.err) is set."""
         M, N, K, epi = self.M, self.N, self.K, self.epi
         layout, rows, waves = cfg or self.cfg
         _check(x, "x", BF16, (M, K))
@@ -205,17 +206,20 @@ class Gemv:
                 _check(sin, "sin", BF16)
                 _check(rope_out, "rope", BF16, (M, 2, cos.shape[1]))
             if ring is not None:
-                host, ctr = ring
+                _need(len(ring) in (2, 3), "ring is (host, ctr) or (host, ctr, err)")
+                host, ctr = ring[:2]
                 _need(isinstance(host, torch.Tensor) and host.dtype == torch.int64
                       and not host.is_cuda and host.is_pinned() and host.is_contiguous()
                       and host.dim() == 2 and host.shape[1] == M,
                       "ring host must be a pinned contiguous int64 [R, M] CPU tensor")
                 _check(ctr, "ring counter", torch.int32, (M,))
+                if len(ring) == 3 and ring[2] is not None:
+                    _check(ring[2], "ring err", torch.int32, (1,))
         part = (self._scratch(x.device, (layout, rows, waves))
                 if epi == EPI_ARGMAX or (layout == 3 and rows > 1) or layout == 4 else None)
         if epi == EPI_ARGMAX and (rope is not None or ring is not None):
             cos, sin, rope_out = rope if rope is not None else (None, None, None)
-            host, ctr = ring if ring is not None else (None, None)
+            host, ctr, err = (tuple(ring) + (None,))[:3] if ring is not None else (None,) * 3
             _lib.call("ko_lm_head_argmax", _lib.ptr(x), _lib.ptr(w),
                       _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,
                       _lib.ptr(y), _lib.ptr(ids), _lib.ptr(pos_inc), _lib.ptr(next_emb),
@@ -224,8 +228,8 @@ class Gemv:
                       _lib.ptr(rope_out),
                       None if host is None else _lib.host_device_ptr(host),
                       0 if host is None else host.shape[0],
-                      _lib.ptr(ctr), _lib.ptr(part), part.numel(), M, N, K, layout, rows, waves,
-                      self.eps, _lib.stream_ptr())
+                      _lib.ptr(ctr), _lib.ptr(err), _lib.ptr(part), part.numel(), M, N, K,
+                      layout, rows, waves, self.eps, _lib.stream_ptr())
             return
         _lib.call("ko_gemv", _lib.ptr(x), _lib.ptr(w), _lib.ptr(y),
                   _lib.ptr(nw) if self.norm else None, _lib.ptr(ss) if self.norm else None,

@@ -16,12 +16,6 @@ def bf(x):
     return x.to(BF16).to(F32)
 
 
-def rms_rstd(x, eps):
-    """rsqrt(mean(x^2) + eps) over the last dim, fp32 (modeling_qwen3.py Qwen3RMSNorm)."""
-    xf = x.to(F32)
-    return torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-
-
 def add_rms_norm(res, delta, weight, eps):
     """engine/kernels/fused.py:16-36. Returns (new_res bf16, out bf16).
 

@@ -475,7 +475,11 @@ def test_decode_qkv_oproj_equals_attention_then_o_gemv(dev, B, cap, pos0):
         for _ in range(steps - 1):
             graph.replay()
         torch.cuda.synchronize()
-        assert torch.all(att.counters == 0) and torch.all(att.sync == 0)
+        assert torch.all(att.counters == 0)
+        if fused_launch:
+            # every group word holds (launches so far, 0 workgroups started)
+            words = att.sync[32:].view(32, 32)[:, 16:18].cpu()
+            assert torch.all(words[:, 0] == 0) and torch.all(words[:, 1] == steps), words
         assert int(att.err.item()) == 0, "the o projection's wait gave up"
         return out.cpu(), h.cpu(), k.cpu(), v.cpu()
 

@@ -15,11 +15,12 @@ TIE_MARGIN = 2.0
 LOGIT_ATOL = 0.25
 # Full 36-layer depth, random N(0, 0.02) weights, hundreds of decode steps: the
 # reference eager path is itself 0.20-0.22 logits away from its own replay with
-# other GEMM shapes (decode-shaped against prefill-shaped), so the stated bar is
-# a flat 0.35 logits, and at least 85 % of the tokens must be the reference's
-# greedy choice (measured 0.90-0.94; the rest are near-ties within the 2x-error
-# rule).
+# other GEMM shapes (decode-shaped against prefill-shaped). The bar is both a
+# flat 0.35 logits and 1.5x that self-noise (+0.02), and at least 85 % of the
+# tokens must be the reference's greedy choice (measured 0.89-0.95; the rest
+# are near-ties within the 2x-error rule).
 FULL_LOGIT_ATOL = 0.35
+FULL_NOISE_FACTOR, FULL_NOISE_SLACK = 1.5, 0.02
 FULL_AGREEMENT_MIN = 0.85
 
 
@@ -143,6 +144,7 @@ def test_engine_full_size_decode(dev, B, S, n):
           f"{agree_p:.4f}), max |dlogit| {err:.4f}; reference decode- vs prefill-shaped "
           f"{ref_noise:.4f}")
     assert err <= FULL_LOGIT_ATOL
+    assert err <= FULL_NOISE_FACTOR * ref_noise + FULL_NOISE_SLACK
     assert agree >= FULL_AGREEMENT_MIN
 
 
@@ -216,11 +218,13 @@ def test_fused_decode_graph_above_16_rows(dev, B):
     assert err < LOGIT_ATOL
 
 
-def test_auto_keeps_the_faster_decode_graph(dev):
+def test_timed_choice_keeps_the_faster_decode_graph(dev):
+    """decode_graph="timed" captures both decode graphs, times them at setup and
+    keeps the faster (the reference's rule, engine.py:197-208)."""
     cfg = SMALL
     w = perturbed_weights(cfg, seed=11)
     prompt = torch.randint(0, cfg.vocab, (2, 16), generator=torch.Generator().manual_seed(12))
-    eng = _engine(cfg, w, decode_graph="auto")
+    eng = _engine(cfg, w, decode_graph="timed")
     toks, logits = eng.trace(prompt.tolist(), 6)
     t = eng.step_times
     assert set(t) == {"fused_ms", "hipblaslt_ms"}
@@ -230,17 +234,37 @@ def test_auto_keeps_the_faster_decode_graph(dev):
     assert agree == 1.0 and err < LOGIT_ATOL
 
 
-def test_batch_above_the_fused_limit_takes_hipblaslt(dev):
-    """B = FUSED_MAX_B + 1 = 65 sequences: auto selection sets
-    up only the hipBLASLt graph (the reference's rule, engine.py:197-199), and
-    every sequence's tokens and logits meet the oracle replay's bar."""
+def test_auto_builds_one_decode_graph(dev):
+    """decode_graph="auto" (the default) captures only the fused-GEMV graph up to
+    FUSED_MAX_B sequences: no hipBLASLt graph is built or timed."""
     from kernel_optim_amd.engine import FUSED_MAX_B
     cfg = SMALL
+    w = perturbed_weights(cfg, seed=11)
+    for B in (1, FUSED_MAX_B):
+        prompt = torch.randint(0, cfg.vocab, (B, 16), generator=torch.Generator().manual_seed(B))
+        eng = _engine(cfg, w, decode_graph="auto")
+        toks, logits = eng.trace(prompt.tolist(), 4)
+        assert eng.step_kind == "fused" and eng.step_times == {}
+        assert not hasattr(eng, "gu_mm"), "the hipBLASLt graph's buffers were allocated"
+        replay = Qwen3Oracle(cfg, w, B=B, cap=32).teacher_forced(prompt, toks)
+        agree, err = check_against_replay(toks, logits, replay)
+        assert err < LOGIT_ATOL
+        del eng
+
+
+@pytest.mark.parametrize("kind", ["auto", "timed"])
+def test_batch_above_the_fused_limit_takes_hipblaslt(dev, kind):
+    """Above the fused limit only the hipBLASLt graph is set up: B = FUSED_MAX_B + 1
+    (33) with auto, B = FUSED_MAX_TIMED + 1 (65) with the timed choice (the
+    reference's rule, engine.py:197-199), and every sequence's tokens and logits
+    meet the oracle replay's bar."""
+    from kernel_optim_amd.engine import FUSED_MAX_B, FUSED_MAX_TIMED
+    cfg = SMALL
     w = perturbed_weights(cfg, seed=13)
-    B = FUSED_MAX_B + 1
+    B = (FUSED_MAX_B if kind == "auto" else FUSED_MAX_TIMED) + 1
     prompt = torch.randint(0, cfg.vocab, (B, 24), generator=torch.Generator().manual_seed(14))
     n = 5
-    eng = _engine(cfg, w, decode_graph="auto")
+    eng = _engine(cfg, w, decode_graph=kind)
     toks, logits = eng.trace(prompt.tolist(), n)
     assert eng.step_kind == "hipblaslt" and eng.step_times == {}
     replay = Qwen3Oracle(cfg, w, B=B, cap=32).teacher_forced(prompt, toks)
@@ -264,3 +288,51 @@ def test_generate_short_outputs(dev, n, spec):
     assert len(out) == n and all(isinstance(x, list) and len(x) == 3 for x in out)
     toks, _ = eng.trace(prompt.tolist(), n)
     assert torch.equal(torch.tensor(out).T, toks)
+
+
+def test_generate_stopped_early_then_called_again(dev):
+    """A caller that stops reading generate() after 3 tokens (the generator not
+    closed, a replay possibly still queued) and calls it again at once with the
+    same shape gets exactly a fresh engine's tokens: nothing of the first call
+    lands in the second call's id ring."""
+    from kernel_optim_amd.engine import Engine
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=41)
+    prompt = torch.randint(0, cfg.vocab, (1, 33), generator=torch.Generator().manual_seed(42)).tolist()
+    eng = Engine.from_weights(cfg, w, decode_graph="fused")
+    first = eng.generate(prompt, 10)
+    head = [next(first) for _ in range(3)]
+    again = list(eng.generate(prompt, 10))
+    del first
+    fresh = list(Engine.from_weights(cfg, w, decode_graph="fused").generate(prompt, 10))
+    assert again == fresh and head == fresh[:3]
+
+
+def test_oproj_wait_giveup_stops_generation_at_that_step(dev):
+    """A failed wait of the attention + o projection launch, forced from the host
+    with a poll limit of 0 (every kernel still runs to its end; only the results
+    are invalid): generate() yields the prefill's token and raises at the first
+    decode step, with no later token, and trace() raises at that step too. The
+    error clears the failure flag and the sync words, and the next call (with the
+    library's poll bound) decodes exactly as a fresh engine."""
+    from kernel_optim_amd.engine import Engine
+    cfg = SMALL
+    w = perturbed_weights(cfg, seed=43)
+    prompt = torch.randint(0, cfg.vocab, (1, 40), generator=torch.Generator().manual_seed(44)).tolist()
+    fresh = list(Engine.from_weights(cfg, w, decode_graph="fused").generate(prompt, 6))
+    eng = Engine.from_weights(cfg, w, decode_graph="fused", keep_logits=True)
+    eng.oproj_spin = 0
+    gen = eng.generate(prompt, 6)
+    assert next(gen) == fresh[0]
+    assert eng.attn.oproj_fusable(), "this test needs the attention + o projection launch"
+    with pytest.raises(RuntimeError, match="timed out"):
+        next(gen)
+    assert list(gen) == []
+    assert int(eng.attn.err.item()) == 0 and torch.all(eng.attn.sync == 0)
+    with pytest.raises(RuntimeError, match="timed out"):
+        eng.trace(prompt, 4)
+    eng.oproj_spin = -1
+    eng._shape = None   # capture again with the library's poll bound
+    assert list(eng.generate(prompt, 6)) == fresh
+    toks, _ = eng.trace(prompt, 6)
+    assert torch.equal(toks, torch.tensor(fresh).T)
