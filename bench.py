@@ -147,12 +147,13 @@ def bench_decode(args, eng=None, B=1):
         pass
     torch.cuda.synchronize()
     t0 = None
-    out = []
+    steps = []
     for i, toks in enumerate(eng.generate(prompt, N)):
         if i == 0:
             t0 = time.perf_counter()
-        out.append(toks[0])
+        steps.append(toks)
     el = time.perf_counter() - t0
+    out = [t[0] for t in steps]
     tok_s = B * (N - 1) / el
     step_ms = eng.time_step(min(50, N - 1))
     kv_per_key = cfg.layers * 2 * cfg.nkv * cfg.head_dim * 2
@@ -179,12 +180,66 @@ def bench_decode(args, eng=None, B=1):
     }
     if eng.step_kind == "fused":
         res["gemv_cfg"] = {k: [list(g.cfg), round(g.us, 2)] for k, g in eng.gv.items()}
-    if not args.no_cpu and B == 1:
-        cb = cpu_decode_baseline(eng, prompt, args.cpu_seconds)
-        if "first_token" in cb:   # the prefill's greedy token, on both paths
-            cb["first_token_matches_gpu"] = cb["first_token"] == out[0]
+    if not args.no_cpu:
+        hf = hf_cpu_model(args, eng)
+        if hf is not None:
+            # the contract's quality rule: the emitted tokens replayed teacher-forced
+            # through native Qwen (Transformers, CPU), one full forward per sequence
+            seqs = list(range(min(B, 2)))
+            res["quality"] = hf_teacher_forced_quality(hf, prompt, steps, seqs)
+        if B == 1:
+            cb = cpu_decode_baseline(eng, prompt, args.cpu_seconds, hf)
+            if "first_token" in cb:   # the prefill's greedy token, on both paths
+                cb["first_token_matches_gpu"] = cb["first_token"] == out[0]
+        else:
+            cb = cpu_decode_baseline_cached(eng, hf, B, S, args.cpu_seconds)
         res["cpu_baseline"] = cb
     return res
+
+
+def hf_cpu_model(args, eng):
+    """Transformers' Qwen3ForCausalLM on the CPU with the engine's weights, built
+    once per run (None where Transformers is not importable)."""
+    if getattr(args, "_hf", None) is None:
+        try:
+            from kernel_optim_amd.model import weights_to
+            args._hf = hf_qwen3_cpu(eng.cfg, weights_to(eng.w, "cpu"))
+        except ImportError:
+            args._hf = False
+    return args._hf or None
+
+
+def hf_teacher_forced_quality(m, prompt, steps, seqs, margin=2.0):
+    """The reference contract's quality check (QWEN_ENGINE_CONTRACT.md, "The
+    quality rule"): each emitted token must be native Qwen's argmax given the
+    tokens emitted before it, or within ``margin`` logits of it. Native Qwen here
+    is Transformers' Qwen3ForCausalLM (sdpa, bf16) on the CPU with the same
+    weights; sequence b's prompt and its first N-1 emitted tokens go through one
+    forward and the logits of the last N positions are compared. ``steps``: the
+    N yielded lists of B ids; ``seqs``: the sequences replayed."""
+    import torch
+    N = len(steps)
+    toks = torch.tensor(steps, dtype=torch.int64).T          # [B, N]
+    agree = total = over = 0
+    worst = 0.0
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        for b in seqs:
+            ids = torch.tensor([list(prompt[b]) + toks[b, :N - 1].tolist()], dtype=torch.int64)
+            lg = m(input_ids=ids, logits_to_keep=N).logits[0].float()   # [N, V]
+            chosen = lg.gather(1, toks[b][:, None])[:, 0]
+            gap = lg.max(-1).values - chosen
+            agree += int((lg.argmax(-1) == toks[b]).sum())
+            total += N
+            over += int((gap > margin).sum())
+            worst = max(worst, float(gap.max()))
+    return {"judge": "teacher-forced replay through Transformers Qwen3ForCausalLM (sdpa, "
+                     "bf16, CPU), one forward per sequence",
+            "sequences": len(seqs), "positions": total,
+            "greedy_agreement": round(agree / total, 4),
+            "max_gap_to_argmax_logits": round(worst, 4), "tie_margin_logits": margin,
+            "positions_over_margin": over, "pass": over == 0,
+            "replay_s": round(time.perf_counter() - t0, 1)}
 
 
 def bench_spec(args, eng, B=1):
@@ -309,7 +364,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     return res
 
 
-def cpu_decode_baseline(eng, prompt, seconds):
+def cpu_decode_baseline(eng, prompt, seconds, m=None):
     """The reference's CPU path for the decode workload: Transformers'
     Qwen3ForCausalLM (sdpa attention) in bf16 with the engine's weights, greedy
     with a DynamicCache on the same 1024-token prompt; the prefill is timed on
@@ -318,12 +373,9 @@ def cpu_decode_baseline(eng, prompt, seconds):
     where Transformers is not importable."""
     import torch
     from kernel_optim_amd.model import weights_to
-    w = weights_to(eng.w, "cpu")
-    try:
-        from transformers import DynamicCache
-        m = hf_qwen3_cpu(eng.cfg, w)
-    except ImportError:
-        return cpu_decode_baseline_port(eng, w, seconds)
+    if m is None:
+        return cpu_decode_baseline_port(eng, weights_to(eng.w, "cpu"), seconds)
+    from transformers import DynamicCache
     ids = torch.tensor(prompt, dtype=torch.int64)
     with torch.inference_mode():
         t0 = time.perf_counter()
@@ -339,7 +391,6 @@ def cpu_decode_baseline(eng, prompt, seconds):
             el = time.perf_counter() - t0
             if el >= seconds or n >= 255:
                 break
-    del m, w
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": torch.get_num_threads(),
             "kind": "reference",
             "prefill_s": round(prefill_s, 3), "first_token": first,
@@ -347,6 +398,148 @@ def cpu_decode_baseline(eng, prompt, seconds):
                       f"(sdpa), bf16, the same 36-layer weights, B=1, the same 1024-token "
                       f"prompt with a DynamicCache: prefill {prefill_s:.1f} s, then {n} greedy "
                       f"decode steps in {el:.1f} s; {torch.get_num_threads()} threads, affinity "
+                      f"{len(os.sched_getaffinity(0))} cpus"}
+
+
+def _random_cache(cfg, B, S, layers):
+    """A DynamicCache holding S random bf16 keys and values per layer (the
+    decode step's cost does not depend on their values)."""
+    import torch
+    from transformers import DynamicCache
+    cache = DynamicCache()
+    g = torch.Generator().manual_seed(5)
+    for i in range(layers):
+        k = torch.empty(B, cfg.nkv, S, cfg.head_dim, dtype=torch.bfloat16)
+        k.copy_(torch.randn(k.shape, generator=g))
+        cache.update(k, k.clone(), i)
+    return cache
+
+
+def cpu_decode_baseline_cached(eng, m, B, S, seconds):
+    """The reference's CPU path for batched decode: Transformers'
+    Qwen3ForCausalLM (sdpa, bf16) with the engine's weights, greedy one-token
+    steps of B sequences from a DynamicCache already holding S keys per
+    sequence and layer (random values: the B x S-token prefill alone would take
+    minutes on the host), for about ``seconds``."""
+    import torch
+    if m is None:
+        return None
+    cache = _random_cache(eng.cfg, B, S, eng.cfg.layers)
+    tok = torch.randint(0, eng.cfg.vocab, (B, 1), generator=torch.Generator().manual_seed(6))
+    with torch.inference_mode():
+        out = m(input_ids=tok, past_key_values=cache, use_cache=True)      # warm
+        tok = out.logits[:, -1].float().argmax(-1, keepdim=True)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            out = m(input_ids=tok, past_key_values=cache, use_cache=True)
+            tok = out.logits[:, -1].float().argmax(-1, keepdim=True)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 255:
+                break
+    del cache
+    return {"value": round(B * n / el, 3), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "sample": f"Transformers {__import__('transformers').__version__} Qwen3ForCausalLM "
+                      f"(sdpa), bf16, the same {eng.cfg.layers}-layer weights, B={B} greedy one-token decode "
+                      f"steps from a DynamicCache of {S} random keys per sequence, {n} steps "
+                      f"in {el:.1f} s; {torch.get_num_threads()} threads, affinity "
+                      f"{len(os.sched_getaffinity(0))} cpus"}
+
+
+def cpu_layer_baseline(cfg, Bs, ctx, seconds):
+    """The reference's CPU path for one decoder layer's decode step:
+    Transformers' Qwen3DecoderLayer (sdpa, bf16, weights N(0, 0.02)) at B
+    sequences over a DynamicCache of ``ctx`` random keys, one new token at
+    position ctx (its K/V appended, then cropped away again), for about
+    ``seconds`` per batch size; us per layer and GB/s of the GPU leg's bytes."""
+    import torch
+    from transformers import Qwen3Config as HC
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer, Qwen3RotaryEmbedding
+    hc = HC(hidden_size=cfg.hidden, intermediate_size=cfg.inter, num_hidden_layers=1,
+            num_attention_heads=cfg.nq, num_key_value_heads=cfg.nkv, head_dim=cfg.head_dim,
+            vocab_size=cfg.vocab, rms_norm_eps=cfg.eps, rope_theta=cfg.theta,
+            max_position_embeddings=40960, attn_implementation="sdpa")
+    layer = Qwen3DecoderLayer(hc, layer_idx=0).to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(7)
+    with torch.no_grad():
+        for p in layer.parameters():
+            if p.dim() == 2:
+                p.copy_(0.02 * torch.randn(p.shape, generator=g))
+    rot = Qwen3RotaryEmbedding(hc)
+    res = {}
+    for B in Bs:
+        cache = _random_cache(cfg, B, ctx, 1)
+        hs = torch.randn(B, 1, cfg.hidden, generator=g).to(torch.bfloat16)
+        pid = torch.full((B, 1), ctx, dtype=torch.int64)
+        with torch.inference_mode():
+            pe = rot(hs, pid)
+            step = lambda: (layer(hs, attention_mask=None, position_ids=pid, past_key_values=cache,
+                                  use_cache=True, position_embeddings=pe), cache.crop(-1))
+            step()
+            n, t0 = 0, time.perf_counter()
+            while True:
+                step()
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= seconds:
+                    break
+        us = el / n * 1e6
+        nbytes = cfg.layer_bytes() + B * (ctx + 1) * cfg.nkv * cfg.head_dim * 2 * 2 + \
+            B * cfg.nkv * cfg.head_dim * 2 * 2
+        res[f"B{B}"] = {"us_per_layer": round(us, 1), "gbs": round(nbytes / us / 1e3, 3),
+                        "calls": n}
+        del cache
+    return {"value": res, "unit": "us per layer", "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "sample": f"Transformers {__import__('transformers').__version__} Qwen3DecoderLayer "
+                      f"(sdpa), bf16, one token at position {ctx} over {ctx} cached keys, "
+                      f"B = {', '.join(str(b) for b in Bs)}, about {seconds:.0f} s each; "
+                      f"{torch.get_num_threads()} threads, affinity "
+                      f"{len(os.sched_getaffinity(0))} cpus"}
+
+
+def cpu_ragged_baseline(seconds):
+    """The reference's CPU path for the ragged attention workload: torch SDPA
+    in bf16 with enable_gqa (Transformers' sdpa decode attention) per sequence
+    over its valid keys only, the same 64 lengths as the GPU leg; whole passes
+    over the 64 sequences for about ``seconds``; GB/s of the valid bytes."""
+    import torch
+    import torch.nn.functional as F
+    Bg = 64
+    lens = torch.randint(128, 16385, (Bg,), generator=torch.Generator().manual_seed(3),
+                         dtype=torch.int32).tolist()
+    g = torch.Generator().manual_seed(4)
+    flat = torch.empty(2 * NKV * D * sum(lens), dtype=torch.bfloat16)
+    for i in range(0, flat.numel(), 1 << 26):
+        seg = flat[i:i + (1 << 26)]
+        seg.copy_(torch.randn(seg.shape, generator=g))
+    kv, off = [], 0
+    for L in lens:
+        n = NKV * L * D
+        kv.append((flat[off:off + n].view(1, NKV, L, D), flat[off + n:off + 2 * n].view(1, NKV, L, D)))
+        off += 2 * n
+    q = torch.randn(Bg, 1, NQ, 1, D, generator=g).to(torch.bfloat16)
+
+    def one_pass():
+        for b, (k, v) in enumerate(kv):
+            F.scaled_dot_product_attention(q[b], k, v, scale=D ** -0.5, enable_gqa=True)
+
+    one_pass()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        one_pass()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    nbytes = 4096 * sum(lens) + 2 * Bg * NQ * D * 2
+    del flat, kv
+    return {"value": round(nbytes * n / el / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "reference",
+            "sample": f"torch scaled_dot_product_attention, bf16, enable_gqa, per sequence over "
+                      f"its valid keys (B = 64, lengths U[128, 16384], seed 3, {sum(lens)} keys), "
+                      f"{n} passes in {el:.1f} s; {torch.get_num_threads()} threads, affinity "
                       f"{len(os.sched_getaffinity(0))} cpus"}
 
 
@@ -547,10 +740,20 @@ def main():
         line["decode_b1_spec"] = bench_spec(args, eng, B=1)
         del eng
         torch.cuda.empty_cache()
+    args._hf = None
     if not args.no_attn and not args.no_ragged:
         line["attention_ragged_b64"] = bench_attention_ragged()
+        if not args.no_cpu:
+            line["attention_ragged_b64"]["cpu_baseline"] = cpu_ragged_baseline(args.cpu_seconds / 2)
     if not args.no_layer:
         line["layer_2048"] = bench_layer()
+        if not args.no_cpu:
+            from kernel_optim_amd.model import Qwen3Config
+            try:
+                line["layer_2048"]["cpu_baseline"] = cpu_layer_baseline(
+                    Qwen3Config(), (1, 4, 16), 2048, args.cpu_seconds / 4)
+            except ImportError:
+                pass
     print(json.dumps(line), flush=True)
 
 
