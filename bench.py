@@ -288,8 +288,8 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
     cannot serve a replay; the replays are captured in one graph and timed with
     events."""
     import torch
-    from kernel_optim_amd.engine import (_rope_tables, attn_units_per_seq, build_decode_gemvs,
-                                         decode_layer)
+    from kernel_optim_amd.engine import (OPROJ_DELAY_NS, _rope_tables, attn_units_per_seq,
+                                         build_decode_gemvs, decode_layer)
     from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
     from kernel_optim_amd.kernels.gemv import tile_weights
     from kernel_optim_amd.model import Qwen3Config, random_weights
@@ -322,7 +322,7 @@ def bench_layer(Bs=(1, 4, 16), ctx=2048, nsets=4, reps=30):
         # o projection in the attention's launch where it fits (B <= 2)
         att = DecodeAttention(B, 1, cap, cfg.nq, cfg.nkv, cfg.head_dim, dev, fused_combine=True,
                               units_per_seq=attn_units_per_seq(B, cfg.nkv))
-        att.oproj_delay_ns = 500
+        att.oproj_delay_ns = OPROJ_DELAY_NS
         rope = torch.empty(B, 2, cfg.head_dim, device=dev, dtype=torch.bfloat16)
         fuse_o = att.oproj_fusable()
         ops, W = build_decode_gemvs(cfg, B, raw, time.monotonic() + 20, tiled_fn)

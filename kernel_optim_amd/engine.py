@@ -54,7 +54,10 @@ TUNE = os.environ.get("ENGINE_TUNE", "1") == "1"
 TUNE_BUDGET_S = 60.0
 # attention and the o projection in one launch for 1-2 sequences (ENGINE_FUSE_OPROJ=0: two)
 FUSE_OPROJ = os.environ.get("ENGINE_FUSE_OPROJ", "1") == "1"
-OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "500"))
+# how long the o projection's workgroups hold their weight loads so the attention's
+# first loads go ahead (B = 1 decode, same box: 250 ns 564.9, 500 ns 569.0, 750-1100 ns
+# 572-575, 1500 ns 569.1, 2000 ns 564.7, 3000 ns 558.2 tok/s)
+OPROJ_DELAY_NS = int(os.environ.get("ENGINE_OPROJ_DELAY_NS", "1000"))
 # keys per decode-attention unit (0: DecodeAttention's sizing rule)
 ATTN_UNIT = int(os.environ.get("ENGINE_ATTN_UNIT", "0"))
 # units per sequence of the one-token attention at B >= 3 (-1: one round of the

@@ -19,7 +19,7 @@ import time
 import pytest
 import torch
 
-from kernel_optim_amd.engine import build_decode_gemvs, decode_layer
+from kernel_optim_amd.engine import OPROJ_DELAY_NS, build_decode_gemvs, decode_layer
 from kernel_optim_amd.kernels.fused import DecodeAttention, rope_rows
 from kernel_optim_amd.model import Qwen3Config, random_weights
 from oracle import attention as A
@@ -49,7 +49,7 @@ def test_decoder_layer_2048_cached_keys(dev, B):
     raw = {name: [lw[name]] for name in ("qkv", "o", "gu", "down")}
     gv, W = build_decode_gemvs(cfg, B, raw, time.monotonic() + 30)
     attn = DecodeAttention(B, 1, cap, nq, nkv, d, dev, fused_combine=True)
-    attn.oproj_delay_ns = 500
+    attn.oproj_delay_ns = OPROJ_DELAY_NS
     cos, sin = orc.cos, orc.sin
     pos = torch.full((B,), CTX, dtype=torch.int32, device=dev)
     rope = torch.empty(B, 2, d, dtype=torch.bfloat16, device=dev)
