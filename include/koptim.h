@@ -68,8 +68,8 @@ int ko_decode_attn(const void* q, const void* k_cache, const void* v_cache, cons
 /* ko_decode_attn in its two-launch form (partials, then the log-sum-exp
  * combine) with no caller scratch and no allocation: the fp32 partials live in
  * a fixed 16 MiB device array of the library (one per GPU, held until the
- * process ends; its address is looked up on the first call on each device).
- * No counterpart in the reference: for callers that cannot allocate (code
+ * process ends; its address is looked up on the first call on each device,
+ * which may itself be made under graph capture). No counterpart in the reference: for callers that cannot allocate (code
  * under hipGraph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Rejects with KO_ERANGE, before launching anything, a call whose
  * partials exceed the array: B*T*nq*max_units*(head_dim + 2) floats (plus up

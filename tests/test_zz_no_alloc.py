@@ -5,7 +5,15 @@ caller's scratch (the same kernels: bit-equal), through the C ABI:
   3 ragged sequences of a 700-key cache), so the second reuses the array the
   first left behind;
 - a call whose partials do not fit the array is refused on the host before any
-  launch (KO_ERANGE), and the array still serves the next call."""
+  launch (KO_ERANGE), and the array still serves the next call;
+- in a fresh process, the entry point's first call (the one that looks up the
+  array's device address) made under torch CUDA-graph capture, before any other
+  launch of the library; the graph is replayed three times with the scratch
+  form run eagerly between replays, and every replay is bit-equal to it."""
+
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -64,3 +72,48 @@ def test_noalloc_refuses_partials_beyond_its_array(dev):
     assert _noalloc(att, q, k, v, pos, out) == 0
     torch.cuda.synchronize()
     assert torch.equal(out, want)
+
+
+_CAPTURED_FIRST = r'''
+import torch
+from kernel_optim_amd import _lib
+from kernel_optim_amd.kernels.fused import DecodeAttention
+
+dev = torch.device("cuda:0")
+NQ, NKV, D = 32, 8, 128
+B, cap, lens = 3, 700, [700, 1, 333]
+g = torch.Generator(device=dev).manual_seed(4)
+q = torch.randn(B, NQ * D, device=dev, generator=g).to(torch.bfloat16)
+k = torch.randn(B, NKV, cap, D, device=dev, generator=g).to(torch.bfloat16)
+v = torch.randn(B, NKV, cap, D, device=dev, generator=g).to(torch.bfloat16)
+pos = torch.tensor([l - 1 for l in lens], dtype=torch.int32, device=dev)
+att = DecodeAttention(B, 1, cap, NQ, NKV, D, dev)  # no library launch yet
+out = torch.full_like(q, float("nan"))
+torch.cuda.synchronize()
+print("capturing the first ko_decode_attn_noalloc call", flush=True)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    rc = _lib.lib().ko_decode_attn_noalloc(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(pos), 1, cap, k.stride(0), k.stride(1),
+        B, 1, NKV, D, att.unit, att.max_units, att.grid_waves, att.scale, _lib.ptr(out),
+        _lib.stream_ptr())
+print("capture rc", rc, flush=True)
+assert rc == 0, rc
+want = torch.empty_like(q)
+for i in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    att(q, k, v, pos, want)  # the scratch form, eagerly, between replays
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), ("replay", i)
+print("replays bit-equal", flush=True)
+'''
+
+
+def test_noalloc_first_call_under_graph_capture():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    proc = subprocess.run([sys.executable, "-c", _CAPTURED_FIRST], cwd=root, env=env,
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-4000:]
+    assert "replays bit-equal" in proc.stdout
