@@ -35,9 +35,8 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
 
 // bf16(nw * bf16(x * rstd)) on packed pairs (gemv.py:77-79).
 __device__ __forceinline__ uint32_t norm2(uint32_t x, uint32_t w, float rstd) {
-  const float a = bf16lo(w) * round_bf16(bf16lo(x) * rstd);
-  const float b = bf16hi(w) * round_bf16(bf16hi(x) * rstd);
-  return pack_bf16x2(a, b);
+  const uint32_t t = pack_bf16x2(bf16lo(x) * rstd, bf16hi(x) * rstd);  // bf16(x * rstd)
+  return pack_bf16x2(bf16lo(w) * bf16lo(t), bf16hi(w) * bf16hi(t));
 }
 __device__ __forceinline__ uint4 norm8(const uint4& x, const uint4& w, float rstd) {
   return make_uint4(norm2(x.x, w.x, rstd), norm2(x.y, w.y, rstd), norm2(x.z, w.z, rstd),

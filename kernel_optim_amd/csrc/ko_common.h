@@ -35,8 +35,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ float round_bf16(float f) {
   return bf16_to_f32(f32_to_bf16(f));
 }
+// Both halves rounded by one v_cvt_pk_bf16_f32 (a vector conversion; two
+// scalar casts give one conversion per value and a pack).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  const bf16x2 v = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // fp32 += a.lo*b.lo + a.hi*b.hi with bf16 pairs (v_dot2c_f32_bf16). The bf16
