@@ -1,7 +1,8 @@
-"""CPU: the ctypes stub in INTEGRATION.md sizes DecodeAttention's launch exactly as
+"""CPU: the ctypes stub of the repository's integration guide (its ``_geometry``
+code block) sizes DecodeAttention's launch exactly as
 kernel_optim_amd.kernels.fused.DecodeAttention does (kernels/fused.py, attn_geometry),
 so a maintainer who binds the C ABI that way gets the same unit, partial buffers and
-grid. The stub's sizing function is taken from the document's code block itself."""
+grid. The stub's sizing function is taken from the guide's code block itself."""
 
 import ast
 import os
